@@ -1,0 +1,469 @@
+// The exact kernels: ggml-cpu's arm64 routines restated for gfx950 wave64 in
+// ggml's accumulation order, so every output has the same bits as ggml-cpu
+// (StablehloMlx/Kernels/Shaders.lean:55-208 restates the same routines for
+// Metal).  No atomics: every output has one writer and a fixed order, so
+// eager and graph-replayed runs give identical bits.
+#include <hip/hip_runtime.h>
+
+#include "erff_cr.h"
+#include "ggml_expf.h"
+#include "ops.h"
+
+namespace shlo {
+
+namespace {
+
+constexpr int kWave = 64;
+
+__device__ __forceinline__ float4 ld4(const float *p) { return *reinterpret_cast<const float4 *>(p); }
+
+// Orders one wave's LDS writes before its later LDS reads by other lanes.
+__device__ __forceinline__ void wave_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+}
+__device__ __forceinline__ void st4(float *p, float4 v) { *reinterpret_cast<float4 *>(p) = v; }
+
+// ---- dot_general in ggml_vec_dot_f32 order --------------------------------------
+
+// The tail and the final combination shared by every dot kernel: `a` holds the
+// 16 block accumulators; returns the finished output.
+template <int TAIL>
+__device__ __forceinline__ float dot_finish(float a[16], const float *w, int64_t wk, const float *x, int64_t xk,
+                                            int64_t np, int64_t K) {
+  // GGML_F32x4_REDUCE (sum[0]+=sum[2], sum[1]+=sum[3], sum[0]+=sum[1]) and
+  // vaddvq_f32 = (v0+v1)+(v2+v3), Shaders.lean:75-79.
+#pragma unroll
+  for (int l = 0; l < 4; l++) a[l] = a[l] + a[8 + l];
+#pragma unroll
+  for (int l = 0; l < 4; l++) a[4 + l] = a[4 + l] + a[12 + l];
+#pragma unroll
+  for (int l = 0; l < 4; l++) a[l] = a[l] + a[4 + l];
+  float s = (a[0] + a[1]) + (a[2] + a[3]);
+  if (TAIL == kTailPinned) {
+    for (int64_t i = np; i < K; i++) {
+      const float p = w[i * wk] * x[i * xk];
+      s = s + p;
+    }
+  } else {
+    // stock: Shaders.lean:80-90
+    const int64_t tl = K - np;
+    const int64_t nq = tl >= 4 ? (tl & ~(int64_t)3) : 0;
+    for (int64_t i = np; i < np + nq; i++) {
+      const float p = w[i * wk] * x[i * xk];
+      s = s + p;
+    }
+    for (int64_t i = np + nq; i < K; i++) s = __builtin_fmaf(w[i * wk], x[i * xk], s);
+  }
+  return s;
+}
+
+// One thread per output; any strides.  The reference kernel's mapping
+// (one thread per output, Shaders.lean:60-64), used for small and irregular
+// shapes and as the parity baseline.
+template <int TAIL>
+__global__ void __launch_bounds__(256) dot_ggml_simple(int64_t n_out, int64_t N, int64_t M, int64_t K,
+                                                       const float *__restrict__ L, int64_t lb, int64_t ln, int64_t lk,
+                                                       const float *__restrict__ R, int64_t rb, int64_t rm, int64_t rk,
+                                                       float *__restrict__ y) {
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n_out; i += (int64_t)gridDim.x * blockDim.x) {
+    const int64_t m = i % M, t = i / M, n = t % N, b = t / N;
+    const float *x = L + b * lb + n * ln;
+    const float *w = R + b * rb + m * rm;
+    if (TAIL == kTailPlain) {  // planted: sequential binary32 sum, no FMA (Shaders.lean:65-68)
+      float s = 0.0f;
+      for (int64_t k = 0; k < K; k++) {
+        const float p = w[k * rk] * x[k * lk];
+        s = s + p;
+      }
+      y[i] = s;
+      continue;
+    }
+    float a[16];
+#pragma unroll
+    for (int j = 0; j < 16; j++) a[j] = 0.0f;
+    const int64_t np = K & ~(int64_t)15;
+    for (int64_t k0 = 0; k0 < np; k0 += 16) {
+#pragma unroll
+      for (int j = 0; j < 16; j++) a[j] = __builtin_fmaf(w[(k0 + j) * rk], x[(k0 + j) * lk], a[j]);
+    }
+    y[i] = dot_finish<TAIL>(a, w, rk, x, lk, np, K);
+  }
+}
+
+// ---- soft_max ---------------------------------------------------------------------
+
+// One wave per row.  Lane l owns the four-element groups g = l + 64j, loaded
+// as float4 (coalesced).  The row maximum is a wave reduction (exact: max is
+// order-free on non-NaN data); each group's e = ggml_v_expf(x*sc - mx) stays in
+// registers; each group's vaddvq_f32 part goes to LDS, and lane 0 adds the
+// parts to a binary64 sum in group order (ggml_vec_soft_max_f32's order,
+// Shaders.lean:111-120).  inv = (float)(1.0/sum), then y = e*inv.
+template <int J>
+__global__ void __launch_bounds__(256) soft_max_k(int64_t rows, int cols, float sc, int float_sum,
+                                                  const float *__restrict__ X, float *__restrict__ Y) {
+  extern __shared__ float lds[];
+  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  const int G = cols / 4;
+  float *parts = lds + wave * ((G + 3) / 4 * 4 + 4);
+  for (int64_t row = blockIdx.x * (int64_t)(blockDim.x / kWave) + wave; row < rows;
+       row += (int64_t)gridDim.x * (blockDim.x / kWave)) {
+    const float *x = X + row * cols;
+    float *y = Y + row * cols;
+    float4 e[J];
+    float mx = -__builtin_inff();
+#pragma unroll
+    for (int j = 0; j < J; j++) {
+      const int g = lane + kWave * j;
+      if (g < G) {
+        e[j] = ld4(x + 4 * g);
+        const float w0 = e[j].x * sc, w1 = e[j].y * sc, w2 = e[j].z * sc, w3 = e[j].w * sc;
+        mx = mx > w0 ? mx : w0;
+        mx = mx > w1 ? mx : w1;
+        mx = mx > w2 ? mx : w2;
+        mx = mx > w3 ? mx : w3;
+      }
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) {
+      const float other = __shfl_xor(mx, o, kWave);
+      mx = mx > other ? mx : other;
+    }
+#pragma unroll
+    for (int j = 0; j < J; j++) {
+      const int g = lane + kWave * j;
+      if (g < G) {
+        e[j].x = ggml_v_expf(e[j].x * sc - mx);
+        e[j].y = ggml_v_expf(e[j].y * sc - mx);
+        e[j].z = ggml_v_expf(e[j].z * sc - mx);
+        e[j].w = ggml_v_expf(e[j].w * sc - mx);
+        parts[g] = (e[j].x + e[j].y) + (e[j].z + e[j].w);
+      }
+    }
+    wave_sync();
+    float inv = 0.0f;
+    if (lane == 0) {
+      if (float_sum) {  // planted: the denominator summed in binary32 (Shaders.lean:120-122)
+        float fs = 0.0f;
+        for (int g = 0; g < G; g++) fs = fs + parts[g];
+        inv = 1.0f / fs;
+      } else {
+        double s = 0.0;
+        int g = 0;
+        for (; g + 4 <= G; g += 4) {
+          const float4 p = ld4(parts + g);
+          s = s + (double)p.x;
+          s = s + (double)p.y;
+          s = s + (double)p.z;
+          s = s + (double)p.w;
+        }
+        for (; g < G; g++) s = s + (double)parts[g];
+        inv = (float)(1.0 / s);
+      }
+    }
+    inv = __shfl(inv, 0, kWave);
+#pragma unroll
+    for (int j = 0; j < J; j++) {
+      const int g = lane + kWave * j;
+      if (g < G) st4(y + 4 * g, make_float4(e[j].x * inv, e[j].y * inv, e[j].z * inv, e[j].w * inv));
+    }
+    wave_sync();
+  }
+}
+
+// ---- norm ---------------------------------------------------------------------------
+
+// One wave per row, the row staged in LDS.  ggml_vec_sum_f32 without
+// Accelerate (a binary64 sum in element order), mean = (float)sum / (float)N,
+// ggml_vec_cvar_f32 (binary64 sum of four-lane groups, then the scalar tail),
+// var = (float)(s2 / N), scale = 1/sqrtf(var + eps), y = (x - mean)*scale
+// (Shaders.lean:147-166).  The sequential sums run on lane 0.
+__global__ void __launch_bounds__(256) norm_k(int64_t rows, int cols, float eps, int gpu_ops,
+                                              const float *__restrict__ X, float *__restrict__ Y) {
+  extern __shared__ float lds[];
+  const int waves = blockDim.x / kWave;
+  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  const int G = cols / 4;
+  float *xr = lds + wave * (cols + 4 + G + 4);
+  float *parts = xr + cols + 4;
+  for (int64_t row = blockIdx.x * (int64_t)waves + wave; row < rows; row += (int64_t)gridDim.x * waves) {
+    const float *x = X + row * cols;
+    float *y = Y + row * cols;
+    for (int i = lane; i < cols; i += kWave) xr[i] = x[i];
+    wave_sync();
+    float mean = 0.0f, scl = 0.0f;
+    if (gpu_ops) {  // planted: binary32 sums and the GPU's own / and sqrt
+      if (lane == 0) {
+        float s = 0.0f;
+        for (int i = 0; i < cols; i++) s = s + xr[i];
+        mean = s / (float)cols;
+        float s2 = 0.0f;
+        for (int i = 0; i < cols; i++) {
+          const float d = xr[i] - mean;
+          s2 = s2 + d * d;
+        }
+        scl = __builtin_amdgcn_rcpf(__builtin_amdgcn_sqrtf(s2 / (float)cols + eps));
+      }
+    } else {
+      if (lane == 0) {
+        double s = 0.0;
+        for (int i = 0; i < cols; i++) s = s + (double)xr[i];
+        mean = (float)s / (float)cols;
+      }
+      mean = __shfl(mean, 0, kWave);
+      for (int g = lane; g < G; g += kWave) {
+        const float d0 = xr[4 * g] - mean, d1 = xr[4 * g + 1] - mean;
+        const float d2 = xr[4 * g + 2] - mean, d3 = xr[4 * g + 3] - mean;
+        const float q0 = d0 * d0, q1 = d1 * d1, q2 = d2 * d2, q3 = d3 * d3;
+        parts[g] = (q0 + q1) + (q2 + q3);
+      }
+      wave_sync();
+      if (lane == 0) {
+        double s2 = 0.0;
+        for (int g = 0; g < G; g++) s2 = s2 + (double)parts[g];
+        for (int i = 4 * G; i < cols; i++) {
+          const float d = xr[i] - mean;
+          const float q = d * d;
+          s2 = s2 + (double)q;
+        }
+        const float var = (float)(s2 / (double)cols);
+        scl = 1.0f / sqrtf(var + eps);
+      }
+    }
+    mean = __shfl(mean, 0, kWave);
+    scl = __shfl(scl, 0, kWave);
+    for (int i = lane; i < cols; i += kWave) y[i] = (xr[i] - mean) * scl;
+    wave_sync();
+  }
+}
+
+// ---- silu -----------------------------------------------------------------------
+
+// x / (1 + ggml_v_expf(0 - x)) on the four-lane body (Shaders.lean:172-179);
+// rows must be multiples of 4 (tails are refused by the lowering).
+__global__ void __launch_bounds__(256) silu_k(int64_t n, int gpu_ops, const float *__restrict__ X,
+                                              float *__restrict__ Y) {
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
+    const float x = X[i];
+    if (gpu_ops) Y[i] = x * __builtin_amdgcn_rcpf(1.0f + __expf(-x));  // planted: GPU exp and /
+    else Y[i] = x / (1.0f + ggml_v_expf(0.0f - x));
+  }
+}
+
+// ---- gelu_erf and the erff map ------------------------------------------------------
+
+constexpr int kPolyWords = erffk::kTab * 6;
+
+__device__ __forceinline__ void load_poly(double *tab) {
+  for (int i = threadIdx.x; i < kPolyWords; i += blockDim.x) tab[i] = (&erffk::kPoly[0][0])[i];
+  __syncthreads();
+}
+
+__device__ __forceinline__ float gelu1(float x, const double *tab, int tanh_form) {
+  float ev;
+  if (tanh_form)  // planted: the tanh form of GELU (Shaders.lean:192-194)
+    ev = tanhf(bits_f(0x3F4C422Au) * x * (1.0f + bits_f(0x3D372713u) * x * x));
+  else
+    ev = erffk::erff_cr(x * bits_f(0x3F3504F3u), tab);  // SQRT_2_INV
+  float y = (0.5f * x) * (1.0f + ev);
+  // A NaN input gives the input quieted, payload kept (Shaders.lean:196-199).
+  if ((f_bits(x) & 0x7FFFFFFFu) > 0x7F800000u) y = bits_f(f_bits(x) | 0x00400000u);
+  return y;
+}
+
+__global__ void __launch_bounds__(256) gelu_erf_k(int64_t n, int tanh_form, const float *__restrict__ X,
+                                                  float *__restrict__ Y) {
+  __shared__ double tab[kPolyWords];
+  load_poly(tab);
+  const int64_t n4 = n / 4;
+  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n4; i += (int64_t)gridDim.x * blockDim.x) {
+    const float4 v = ld4(X + 4 * i);
+    st4(Y + 4 * i, make_float4(gelu1(v.x, tab, tanh_form), gelu1(v.y, tab, tanh_form), gelu1(v.z, tab, tanh_form),
+                               gelu1(v.w, tab, tanh_form)));
+  }
+  for (int64_t i = 4 * n4 + blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
+    Y[i] = gelu1(X[i], tab, tanh_form);
+}
+
+__global__ void __launch_bounds__(256) erff_map_k(uint32_t base, uint32_t count, uint32_t *__restrict__ Y) {
+  __shared__ double tab[kPolyWords];
+  load_poly(tab);
+  for (uint32_t t = blockIdx.x * blockDim.x + threadIdx.x; t < count; t += gridDim.x * blockDim.x)
+    Y[t] = f_bits(erffk::erff_cr(bits_f(base + t), tab));
+}
+
+unsigned grid_cap(int64_t n, int block, int64_t cap) {
+  int64_t g = (n + block - 1) / block;
+  return (unsigned)std::max<int64_t>(1, std::min<int64_t>(g, cap));
+}
+
+}  // namespace
+
+// ---- host side --------------------------------------------------------------------------
+
+namespace {
+int g_default_tail = kTailStock;
+}
+int default_dot_tail() { return g_default_tail; }
+void set_default_dot_tail(int t) {
+  if (t != kTailStock && t != kTailPinned) fail("flavor: 0 (stock) or 1 (pinned)");
+  g_default_tail = t;
+}
+
+ArrayP dot_ggml(const DotOperand &lhs, const DotOperand &rhs, int64_t B, int64_t N, int64_t M, int64_t K, int tail) {
+  if (lhs.arr->dtype != kF32 || rhs.arr->dtype != kF32) fail("dot_general: f32 operands only");
+  if (B < 0 || N < 0 || M < 0 || K < 0) fail("dot_general: negative extent");
+  auto y = new_array(kF32, Shape{B * N * M});
+  const int64_t n_out = B * N * M;
+  if (n_out == 0) return y;
+  if (K > 0 && (!lhs.arr->buf || !rhs.arr->buf)) fail("dot_general: empty operand");
+  const float *L = (const float *)lhs.arr->data();
+  const float *R = (const float *)rhs.arr->data();
+  float *Y = (float *)y->data();
+  ArrayP kl = lhs.arr, kr = rhs.arr;
+  const int64_t lb = lhs.sb, ln = lhs.sf, lk = lhs.sk, rb = rhs.sb, rm = rhs.sf, rk = rhs.sk;
+  const unsigned grid = grid_cap(n_out, 256, 1 << 20);
+  launch([=](hipStream_t s) {
+    (void)kl, (void)kr;
+    switch (tail) {
+      case kTailStock:
+        dot_ggml_simple<kTailStock><<<grid, 256, 0, s>>>(n_out, N, M, K, L, lb, ln, lk, R, rb, rm, rk, Y);
+        break;
+      case kTailPinned:
+        dot_ggml_simple<kTailPinned><<<grid, 256, 0, s>>>(n_out, N, M, K, L, lb, ln, lk, R, rb, rm, rk, Y);
+        break;
+      default:
+        dot_ggml_simple<kTailPlain><<<grid, 256, 0, s>>>(n_out, N, M, K, L, lb, ln, lk, R, rb, rm, rk, Y);
+        break;
+    }
+  });
+  return y;
+}
+
+ArrayP mul_mat(const ArrayP &w0, const ArrayP &x0, int64_t K, int64_t M, int64_t R, int64_t N, int64_t wbs,
+               int tail) {
+  if (N <= 0 || R % N) fail("mul_mat: R must be a multiple of N > 0");
+  ArrayP w = contiguous(w0), x = contiguous(x0);
+  const int64_t B = R / N;
+  if (x->size() < R * K) fail("mul_mat: x holds fewer than R*K elements");
+  if (w->size() < (B - 1) * wbs + M * K) fail("mul_mat: w holds fewer elements than the batch stride needs");
+  return dot_ggml(DotOperand{x, N * K, K, 1}, DotOperand{w, wbs, K, 1}, B, N, M, K, tail);
+}
+
+ArrayP soft_max(const ArrayP &x0, int64_t rows, int64_t cols, uint32_t scale_bits, bool float_sum) {
+  if (x0->dtype != kF32) fail("ggml.soft_max: f32 only");
+  if (rows * cols != x0->size()) fail("ggml.soft_max: rows*cols is not the element count");
+  if (cols % 4)
+    fail(strf("ggml.soft_max: a row of %lld has a %lld-element tail that ggml-cpu sends through the platform "
+              "expf, which is not carried",
+              (long long)cols, (long long)(cols % 4)));
+  if (cols > 4 * kWave * 16) fail("ggml.soft_max: rows above 4096 columns are not carried");
+  ArrayP x = contiguous(x0);
+  auto y = new_array(kF32, x->shape);
+  if (rows == 0 || cols == 0) return y;
+  const float sc = bits_f(scale_bits);
+  const int J = (int)((cols / 4 + kWave - 1) / kWave);
+  const int lds = 4 * (int)((cols / 4 + 3) / 4 * 4 + 4) * (int)sizeof(float);
+  const unsigned grid = grid_cap(rows, 4, 1 << 20);
+  const float *px = (const float *)x->data();
+  float *py = (float *)y->data();
+  const int c = (int)cols;
+  const int fs = float_sum ? 1 : 0;
+  ArrayP kx = x;
+  launch([=](hipStream_t s) {
+    (void)kx;
+    switch (J) {
+#define SM_CASE(n) \
+  case n: soft_max_k<n><<<grid, 256, lds, s>>>(rows, c, sc, fs, px, py); break;
+      SM_CASE(1) SM_CASE(2) SM_CASE(3) SM_CASE(4) SM_CASE(5) SM_CASE(6) SM_CASE(7) SM_CASE(8)
+      SM_CASE(9) SM_CASE(10) SM_CASE(11) SM_CASE(12) SM_CASE(13) SM_CASE(14) SM_CASE(15) SM_CASE(16)
+#undef SM_CASE
+      default: break;
+    }
+  });
+  return y;
+}
+
+ArrayP norm(const ArrayP &x0, int64_t rows, int64_t cols, uint32_t eps_bits, bool gpu_ops) {
+  if (x0->dtype != kF32) fail("ggml.norm: f32 only");
+  if (rows * cols != x0->size()) fail("ggml.norm: rows*cols is not the element count");
+  if (cols > 4096) fail("ggml.norm: rows above 4096 columns are not carried");
+  ArrayP x = contiguous(x0);
+  auto y = new_array(kF32, x->shape);
+  if (rows == 0 || cols == 0) return y;
+  const int lds = 4 * (int)(cols + 4 + cols / 4 + 4) * (int)sizeof(float);
+  const unsigned grid = grid_cap(rows, 4, 1 << 20);
+  const float *px = (const float *)x->data();
+  float *py = (float *)y->data();
+  const float eps = bits_f(eps_bits);
+  const int c = (int)cols, go = gpu_ops ? 1 : 0;
+  ArrayP kx = x;
+  launch([=](hipStream_t s) {
+    (void)kx;
+    norm_k<<<grid, 256, lds, s>>>(rows, c, eps, go, px, py);
+  });
+  return y;
+}
+
+ArrayP silu(const ArrayP &x0, int64_t rows, int64_t cols, bool gpu_ops) {
+  if (x0->dtype != kF32) fail("ggml.silu: f32 only");
+  if (cols % 4)
+    fail(strf("ggml.silu: a row of %lld has a %lld-element tail that ggml-cpu sends through the platform expf, "
+              "which is not carried",
+              (long long)cols, (long long)(cols % 4)));
+  ArrayP x = contiguous(x0);
+  auto y = new_array(kF32, x->shape);
+  const int64_t n = x->size();
+  if (!n) return y;
+  const float *px = (const float *)x->data();
+  float *py = (float *)y->data();
+  const int go = gpu_ops ? 1 : 0;
+  ArrayP kx = x;
+  launch([=](hipStream_t s) {
+    (void)kx;
+    silu_k<<<grid_cap(n, 256, 1 << 16), 256, 0, s>>>(n, go, px, py);
+  });
+  return y;
+}
+
+ArrayP gelu_erf(const ArrayP &x0, bool tanh_form) {
+  if (x0->dtype != kF32) fail("ggml.gelu_erf: f32 only");
+  ArrayP x = contiguous(x0);
+  auto y = new_array(kF32, x->shape);
+  const int64_t n = x->size();
+  if (!n) return y;
+  const float *px = (const float *)x->data();
+  float *py = (float *)y->data();
+  if (((uintptr_t)px | (uintptr_t)py) % 16) fail("ggml.gelu_erf: operands must be 16-byte aligned");
+  const int tf = tanh_form ? 1 : 0;
+  ArrayP kx = x;
+  const unsigned grid = grid_cap(n / 4 + 1, 256, 256 * 8);
+  launch([=](hipStream_t s) {
+    (void)kx;
+    gelu_erf_k<<<grid, 256, 0, s>>>(n, tf, px, py);
+  });
+  return y;
+}
+
+ArrayP erff_map(uint32_t base, uint32_t count) {
+  auto y = new_array(kU32, Shape{(int64_t)count});
+  if (!count) return y;
+  uint32_t *py = (uint32_t *)y->data();
+  launch([=](hipStream_t s) { erff_map_k<<<grid_cap(count, 256, 256 * 16), 256, 0, s>>>(base, count, py); });
+  return y;
+}
+
+ArrayP divide_exact(const ArrayP &a, const ArrayP &b) {
+  if (a->dtype != kF32 || b->dtype != kF32) fail("divide: f32 only");
+  return binary(kDiv, a, b);  // binary32 `/` is correctly rounded on gfx950 (IEEE division sequence)
+}
+
+ArrayP sqrt_exact(const ArrayP &a) {
+  if (a->dtype != kF32) fail("sqrt: f32 only");
+  return unary(kSqrt, a);  // correctly rounded sqrtf (the default HIP lowering)
+}
+
+float erff_host(float x) { return erffk::erff_cr(x, &erffk::kPoly[0][0]); }
+
+}  // namespace shlo

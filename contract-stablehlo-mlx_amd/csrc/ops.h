@@ -1,0 +1,104 @@
+// Array operations: the MI355X counterparts of the mlx-c calls the reference
+// shim makes (c/smlx_shim.c:142-264, :301-323, :388-414) and of the exact
+// kernels its Run.lean dispatches (StablehloMlx/Kernels/Run.lean:155-197).
+#pragma once
+
+#include "runtime.h"
+
+namespace shlo {
+
+// Unary op codes (StablehloMlx/Mlx.lean:274-285).
+enum UnaryOp : uint32_t {
+  kNeg = 0, kAbs = 1, kSqrt = 2, kFloor = 3, kExp = 4, kErf = 5, kNot = 6,
+  kInvert = 7, kRsqrt = 8, kTanh = 9, kSigmoid = 10
+};
+// Binary op codes (StablehloMlx/Mlx.lean:286-307).
+enum BinaryOp : uint32_t {
+  kAdd = 0, kSub = 1, kMul = 2, kDiv = 3, kMax = 4, kMin = 5, kAnd = 6, kOr = 7,
+  kXor = 8, kShl = 9, kShr = 10, kEq = 11, kNe = 12, kLt = 13, kLe = 14, kGt = 15,
+  kGe = 16, kMatmul = 17, kRem = 18, kLAnd = 19, kLOr = 20
+};
+// Internal codes for the planted "built-in" lowerings only: the GPU's
+// reciprocal-based binary32 divide and its raw v_sqrt_f32, neither correctly
+// rounded (the role of MLX's own / and sqrt, Lower.lean:383-390).
+constexpr uint32_t kDivApprox = 100;
+constexpr uint32_t kSqrtApprox = 101;
+
+// ---- views (no device work) -------------------------------------------------
+ArrayP reshape(const ArrayP &a, const Shape &shape);
+ArrayP transpose(const ArrayP &a, const std::vector<int64_t> &perm);
+ArrayP broadcast_to(const ArrayP &a, const Shape &shape);
+ArrayP slice(const ArrayP &a, const Shape &start, const Shape &stop, const Shape &step);
+ArrayP empty_array();
+
+// ---- data movement and elementwise kernels ----------------------------------
+ArrayP contiguous(const ArrayP &a);
+void copy_into(const std::shared_ptr<Array> &dst, const ArrayP &src);  // eager
+ArrayP concat(const std::vector<ArrayP> &xs, int axis);
+ArrayP astype(const ArrayP &a, uint8_t dtype);
+ArrayP view_dtype(const ArrayP &a, uint8_t dtype);
+ArrayP unary(uint32_t op, const ArrayP &a);
+ArrayP binary(uint32_t op, const ArrayP &a, const ArrayP &b);
+ArrayP where(const ArrayP &c, const ArrayP &a, const ArrayP &b);
+ArrayP take(const ArrayP &a, const ArrayP &idx, int axis);
+ArrayP max_axis(const ArrayP &a, int axis);
+ArrayP iota(uint8_t dtype, const Shape &shape, int dim);
+int64_t count_nonzero(const ArrayP &a);
+Shape broadcast_shapes(const Shape &a, const Shape &b);
+
+// Device-side fill from the splitmix32 stream of ref/ggml_ref.c:21-30:
+// dist 0 = unif(param) one draw per element; dist 1 = the Irwin-Hall normal
+// (12 draws per element) times sigma = param.  `skip` draws are skipped first.
+ArrayP fill_random(const Shape &shape, uint32_t seed, uint64_t skip, int dist, double param);
+
+// MLX-style matmul of [..., N, K] x [..., K, M] in a natural (non-ggml) order:
+// the planted "built-in matmul" lowering (StablehloMlx/Lower.lean:177-180).
+ArrayP matmul_builtin(const ArrayP &a, const ArrayP &b);
+
+// ---- the exact ggml kernels -------------------------------------------------
+
+// Tail flavour of ggml_vec_dot_f32 past the last full block of 16
+// (Shaders.lean:80-90; evidence/README.md:41-46).
+enum DotTail : int { kTailStock = 0, kTailPinned = 1, kTailPlain = 2 };
+int default_dot_tail();          // process-wide flavour for dot_general
+void set_default_dot_tail(int);  // 0 stock (the reference kernel), 1 pinned
+
+// One operand of a dot product, addressed as (batch, free, k) with element
+// strides: element (b, f, k) is at data + b*sb + f*sf + k*sk.
+struct DotOperand {
+  ArrayP arr;       // keeps the buffer alive
+  int64_t sb = 0, sf = 0, sk = 0;
+};
+
+// y[(b*N + n)*M + m] = dot over k of lhs(b, n, k) and rhs(b, m, k), each
+// output in ggml_vec_dot_f32's order (16 FMA accumulators over blocks of 16,
+// GGML_F32x4_REDUCE, vaddvq_f32, then the tail).  Output shape [B*N*M].
+ArrayP dot_ggml(const DotOperand &lhs, const DotOperand &rhs, int64_t B, int64_t N, int64_t M,
+                int64_t K, int tail);
+
+// The reference's Run.mulMat surface (Run.lean:155-158): w rows of K, x rows
+// of K; y[r*M + m] = dot(w row (r/N)*wBatchStride/K + m, x row r).
+ArrayP mul_mat(const ArrayP &w, const ArrayP &x, int64_t K, int64_t M, int64_t R, int64_t N,
+               int64_t wBatchStride, int tail);
+
+// ggml soft_max over `rows` rows of `cols` (Shaders.lean:100-123).  cols must
+// be a multiple of 4 unless tails are enabled (the scalar expf is then the
+// correctly rounded one).
+ArrayP soft_max(const ArrayP &x, int64_t rows, int64_t cols, uint32_t scale_bits, bool float_sum);
+// ggml norm (Shaders.lean:130-166).
+ArrayP norm(const ArrayP &x, int64_t rows, int64_t cols, uint32_t eps_bits, bool gpu_ops);
+// ggml silu on rows of `cols` (Shaders.lean:172-179).
+ArrayP silu(const ArrayP &x, int64_t rows, int64_t cols, bool gpu_ops);
+// ggml gelu_erf (Shaders.lean:186-199) with a correctly rounded erff.
+ArrayP gelu_erf(const ArrayP &x, bool tanh_form);
+// y[t] = bits(erff(bits^-1(base + t))), t < count (Shaders.lean:204-208).
+ArrayP erff_map(uint32_t base, uint32_t count);
+// Correctly rounded binary32 / and sqrt (Shaders.lean:213-221).
+ArrayP divide_exact(const ArrayP &a, const ArrayP &b);
+ArrayP sqrt_exact(const ArrayP &a);
+
+// Host copy of the product's erff (the same routine the kernels run), for the
+// CPU side of the exhaustive check (c/smlx_shim.c:388-403).
+float erff_host(float x);
+
+}  // namespace shlo
