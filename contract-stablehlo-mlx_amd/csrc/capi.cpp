@@ -436,6 +436,13 @@ int shlo_fill_random(const int64_t *shape, size_t rank, uint32_t seed, uint64_t 
   });
 }
 
+int shlo_checksum_u32(const shlo_arr *a, uint64_t start_index, uint64_t *out) {
+  return guard("checksum", [&] {
+    need(out, "out");
+    *out = shlo::checksum_u32(A(a), start_index);
+  });
+}
+
 int shlo_sync(void) {
   return guard("sync", [&] { shlo::synchronize(); });
 }

@@ -392,8 +392,12 @@ ArrayP norm(const ArrayP &x0, int64_t rows, int64_t cols, uint32_t eps_bits, boo
   ArrayP x = contiguous(x0);
   auto y = new_array(kF32, x->shape);
   if (rows == 0 || cols == 0) return y;
-  const int lds = 4 * (int)(cols + 4 + cols / 4 + 4) * (int)sizeof(float);
-  const unsigned grid = grid_cap(rows, 4, 1 << 20);
+  // LDS per wave: the row, then its group parts (norm_k's layout); at most
+  // 64 KiB per block.
+  const int per_wave = (int)(cols + 4 + cols / 4 + 4) * (int)sizeof(float);
+  const int waves = std::max(1, std::min(4, 65536 / per_wave));
+  const int lds = waves * per_wave;
+  const unsigned grid = grid_cap(rows, waves, 1 << 20);
   const float *px = (const float *)x->data();
   float *py = (float *)y->data();
   const float eps = bits_f(eps_bits);
@@ -401,7 +405,7 @@ ArrayP norm(const ArrayP &x0, int64_t rows, int64_t cols, uint32_t eps_bits, boo
   ArrayP kx = x;
   launch([=](hipStream_t s) {
     (void)kx;
-    norm_k<<<grid, 256, lds, s>>>(rows, c, eps, go, px, py);
+    norm_k<<<grid, kWave * waves, lds, s>>>(rows, c, eps, go, px, py);
   });
   return y;
 }

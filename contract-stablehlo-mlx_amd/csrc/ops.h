@@ -44,6 +44,8 @@ ArrayP take(const ArrayP &a, const ArrayP &idx, int axis);
 ArrayP max_axis(const ArrayP &a, int axis);
 ArrayP iota(uint8_t dtype, const Shape &shape, int dim);
 int64_t count_nonzero(const ArrayP &a);
+// sum over t of (w[t]+1)*(2(start+t)+1)*0x9E3779B97F4A7C15 mod 2^64 over 32-bit words.
+uint64_t checksum_u32(const ArrayP &a, uint64_t start);
 Shape broadcast_shapes(const Shape &a, const Shape &b);
 
 // Device-side fill from the splitmix32 stream of ref/ggml_ref.c:21-30:

@@ -810,3 +810,46 @@ ArrayP fill_random(const Shape &shape, uint32_t seed, uint64_t skip, int dist, d
 }
 
 }  // namespace shlo
+
+// ---- an order-free checksum of u32 words (test helper) ----------------------------------
+
+namespace shlo {
+namespace {
+
+// sum over t of (w[t] + 1) * (2(start + t) + 1) * 0x9E3779B97F4A7C15 mod 2^64.
+// Integer addition mod 2^64 is associative, so the atomic accumulation is exact.
+__global__ void checksum_u32_k(uint64_t n, uint64_t start, const uint32_t *w, unsigned long long *out) {
+  __shared__ unsigned long long part[kBlock];
+  unsigned long long s = 0;
+  for (uint64_t i = blockIdx.x * (uint64_t)blockDim.x + threadIdx.x; i < n; i += (uint64_t)gridDim.x * blockDim.x)
+    s += ((unsigned long long)w[i] + 1ull) * (2ull * (start + i) + 1ull) * 0x9E3779B97F4A7C15ull;
+  part[threadIdx.x] = s;
+  __syncthreads();
+  for (int k = kBlock / 2; k > 0; k >>= 1) {
+    if ((int)threadIdx.x < k) part[threadIdx.x] += part[threadIdx.x + k];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) atomicAdd(out, part[0]);
+}
+
+}  // namespace
+
+uint64_t checksum_u32(const ArrayP &a0, uint64_t start) {
+  if (tracing()) fail("checksum: not available while a function is being traced");
+  if (dtype_size(a0->dtype) != 4) fail("checksum: 32-bit words only");
+  ArrayP a = contiguous(a0);
+  auto cnt = new_array(kU64, Shape{1});
+  unsigned long long *pc = (unsigned long long *)cnt->data();
+  zero_u64_k<<<1, 1, 0, stream()>>>(pc);
+  check_launch("checksum");
+  const uint64_t n = a->size();
+  if (n) {
+    checksum_u32_k<<<grid_for((int64_t)n), kBlock, 0, stream()>>>(n, start, (const uint32_t *)a->data(), pc);
+    check_launch("checksum");
+  }
+  uint64_t h = 0;
+  array_to_host(cnt, &h);
+  return h;
+}
+
+}  // namespace shlo

@@ -117,7 +117,7 @@ thread_local Trace *g_trace = nullptr;
 }  // namespace
 
 Buffer::~Buffer() {
-  if (ptr) pool().put(ptr, bytes);
+  if (ptr && owned) pool().put(ptr, bytes);
 }
 
 BufferP alloc_buffer(size_t bytes) {
@@ -252,13 +252,40 @@ struct CompiledFn::Variant {
   std::vector<std::shared_ptr<Array>> slots;
   std::vector<std::weak_ptr<const Array>> last_in;
   std::vector<ArrayP> outs;
+  // Buffers handed to the caller by the last apply: they alias the graph's
+  // output buffers (no copy on the common path).
+  std::vector<std::weak_ptr<Buffer>> handed;
   hipGraph_t graph = nullptr;
   hipGraphExec_t exec = nullptr;
-  ~Variant() {
-    if (exec) (void)hipGraphExecDestroy(exec);
-    if (graph) (void)hipGraphDestroy(graph);
-  }
+  ~Variant();
 };
+
+// Outputs of the last apply that the caller still holds move to blocks of
+// their own before the graph overwrites its buffers or the function goes away
+// (their contents are unchanged: arrays stay immutable).
+static void evacuate(CompiledFn::Variant &v) {
+  for (auto &w : v.handed) {
+    if (std::shared_ptr<Buffer> b = w.lock()) {
+      size_t cap = 0;
+      void *p = pool().get(b->bytes, &cap);
+      SHLO_HIP(hipMemcpyAsync(p, b->ptr, b->bytes, hipMemcpyDeviceToDevice, stream()));
+      b->ptr = p;
+      b->bytes = cap;
+      b->owned = true;
+    }
+  }
+  v.handed.clear();
+}
+
+CompiledFn::Variant::~Variant() {
+  try {
+    evacuate(*this);
+  } catch (...) {
+  }
+  (void)hipStreamSynchronize(stream());
+  if (exec) (void)hipGraphExecDestroy(exec);
+  if (graph) (void)hipGraphDestroy(graph);
+}
 
 CompiledFn::~CompiledFn() {
   if (!variants.empty()) (void)hipStreamSynchronize(stream());
@@ -315,6 +342,7 @@ std::vector<ArrayP> apply_fn(CompiledFn &f, const std::vector<ArrayP> &inputs) {
   if (!f.compile || g_trace) return f.fn(inputs);
   CompiledFn::Variant &v = variant_for(f, inputs);
   hipStream_t s = stream();
+  evacuate(v);
   for (size_t i = 0; i < inputs.size(); i++) {
     if (v.last_in[i].lock() == inputs[i]) continue;  // arrays are immutable
     copy_into(v.slots[i], inputs[i]);
@@ -325,8 +353,19 @@ std::vector<ArrayP> apply_fn(CompiledFn &f, const std::vector<ArrayP> &inputs) {
   }
   std::vector<ArrayP> res;
   for (auto &o : v.outs) {
-    auto r = new_array(o->dtype, o->shape);
-    if (r->nbytes()) SHLO_HIP(hipMemcpyAsync(r->data(), o->data(), r->nbytes(), hipMemcpyDeviceToDevice, s));
+    auto r = std::make_shared<Array>();
+    r->dtype = o->dtype;
+    r->shape = o->shape;
+    r->strides = o->strides;
+    r->offset = o->offset;
+    if (o->buf) {
+      auto alias = std::make_shared<Buffer>();
+      alias->ptr = o->buf->ptr;
+      alias->bytes = o->buf->bytes;
+      alias->owned = false;
+      r->buf = alias;
+      v.handed.push_back(alias);
+    }
     res.push_back(r);
   }
   return res;

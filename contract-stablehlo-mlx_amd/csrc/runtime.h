@@ -35,7 +35,8 @@ namespace shlo {
 
 struct Buffer {
   void *ptr = nullptr;
-  size_t bytes = 0;  // capacity handed out by the pool
+  size_t bytes = 0;    // capacity handed out by the pool
+  bool owned = true;   // false: an alias of a compiled function's output buffer
   Buffer() = default;
   Buffer(const Buffer &) = delete;
   Buffer &operator=(const Buffer &) = delete;

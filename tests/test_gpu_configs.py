@@ -1,0 +1,194 @@
+"""GPU parity at the measurement configs: dot_general, softmax
+with a causal mask and erf-GELU, each eager and hipGraph-compiled, bit for
+bit against the oracle; each with its planted wrong lowering."""
+import numpy as np
+import pytest
+
+pytestmark = pytest.mark.gpu
+
+
+def dot_module(N, K, M, batch=0):
+    """[N,K] x [K,M] (contract [1]/[0]); with batch > 0, [B,N,K] x [B,K,M]."""
+    if batch:
+        a, b, o = f"tensor<{batch}x{N}x{K}xf32>", f"tensor<{batch}x{K}x{M}xf32>", f"tensor<{batch}x{N}x{M}xf32>"
+        dn = ("#stablehlo.dot<lhs_batching_dimensions = [0], rhs_batching_dimensions = [0], "
+              "lhs_contracting_dimensions = [2], rhs_contracting_dimensions = [1]>")
+    else:
+        a, b, o = f"tensor<{N}x{K}xf32>", f"tensor<{K}x{M}xf32>", f"tensor<{N}x{M}xf32>"
+        dn = "#stablehlo.dot<lhs_contracting_dimensions = [1], rhs_contracting_dimensions = [0]>"
+    return (f"module {{\n  func.func public @main(%a0: {a}, %a1: {b}) -> ({o}) {{\n"
+            f'    %0 = "stablehlo.dot_general"(%a0, %a1) {{dot_dimension_numbers = {dn}}} : ({a}, {b}) -> {o}\n'
+            f"    func.return %0 : {o}\n  }}\n}}\n")
+
+
+def custom_call_module(target, attrs, shape):
+    t = "tensor<" + "".join(f"{d}x" for d in shape) + "f32>"
+    return (f"module {{\n  func.func public @main(%a0: {t}) -> ({t}) {{\n"
+            f'    %0 = "stablehlo.custom_call"(%a0) {{call_target_name = "{target}", backend_config = "{attrs}"}} : ({t}) -> {t}\n'
+            f"    func.return %0 : {t}\n  }}\n}}\n")
+
+
+def run(text, inputs, faults=0, compile=True):
+    import shlo_hip
+    m = shlo_hip.Module(text)
+    f = m.prepare(faults, compile)
+    return [o.numpy() for o in f.call([shlo_hip.from_numpy(x) for x in inputs])]
+
+
+def oracle_dot(oracle, lhs, rhs, tail):
+    """out[n, m] = dot(lhs[n, :], rhs[:, m]) in ggml order."""
+    return oracle.dot_general_bnk(lhs[None], np.ascontiguousarray(rhs.T)[None], tail)[0]
+
+
+def same_bits(a, b):
+    return a.shape == b.shape and np.array_equal(np.ascontiguousarray(a).view(np.uint32),
+                                                 np.ascontiguousarray(b).view(np.uint32))
+
+
+@pytest.mark.parametrize("flavor", [0, 1])
+def test_dot_config1(oracle, flavor):
+    """[128,256] x [256,512], uniform[-1,1] from seed 1."""
+    import shlo_hip
+    N, K, M = 128, 256, 512
+    lhs, st = oracle.fill_unif(1, 1.0, N * K)
+    rhs, _ = oracle.fill_unif(1, 1.0, K * M, state=st)
+    lhs, rhs = lhs.reshape(N, K), rhs.reshape(K, M)
+    want = oracle_dot(oracle, lhs, rhs, flavor)
+    shlo_hip.set_flavor(flavor)
+    try:
+        for compile in (True, False):
+            got = run(dot_module(N, K, M), [lhs, rhs], compile=compile)[0]
+            assert same_bits(got, want), compile
+        for fault in ("dot_plain", "dot_builtin"):
+            got = run(dot_module(N, K, M), [lhs, rhs], faults=shlo_hip.fault_bits(fault))[0]
+            assert not same_bits(got, want), fault
+    finally:
+        shlo_hip.set_flavor(0)
+
+
+ODD = [1, 7, 33, 257]
+
+
+@pytest.mark.parametrize("K", ODD)
+def test_dot_odd_shapes(oracle, K):
+    """M, N, K in {1, 7, 33, 257}: every tail length and block count, both flavours."""
+    import shlo_hip
+    for N in ODD:
+        for M in ODD:
+            lhs, st = oracle.fill_normal(3, 1.0, N * K)
+            rhs, _ = oracle.fill_normal(3, 1.0, K * M, state=st)
+            lhs, rhs = lhs.reshape(N, K), rhs.reshape(K, M)
+            for flavor in (0, 1):
+                want = oracle_dot(oracle, lhs, rhs, flavor)
+                shlo_hip.set_flavor(flavor)
+                try:
+                    for compile in (True, False):
+                        got = run(dot_module(N, K, M), [lhs, rhs], compile=compile)[0]
+                        assert same_bits(got, want), (N, K, M, flavor, compile)
+                finally:
+                    shlo_hip.set_flavor(0)
+
+
+def test_dot_batched_small(oracle):
+    """A batched dot_general (batch [0]/[0], contract [2]/[1]) at a reduced size."""
+    B, N, K, M = 3, 33, 70, 45
+    lhs, st = oracle.fill_normal(4, 1.0, B * N * K)
+    rhs, _ = oracle.fill_normal(4, 1.0, B * K * M, state=st)
+    lhs, rhs = lhs.reshape(B, N, K), rhs.reshape(B, K, M)
+    want = np.stack([oracle_dot(oracle, lhs[b], rhs[b], 0) for b in range(B)])
+    for compile in (True, False):
+        got = run(dot_module(N, K, M, batch=B), [lhs, rhs], compile=compile)[0]
+        assert same_bits(got, want)
+
+
+def causal_logits(oracle, rows, cols, sigma=4.0, seed=7):
+    x, _ = oracle.fill_normal(seed, sigma, rows * cols)
+    x = x.reshape(rows, cols)
+    mask = np.triu(np.ones((rows, cols), bool), 1)
+    return np.where(mask, np.float32(-np.inf), x).astype(np.float32), mask
+
+
+def test_softmax_config2(oracle):
+    """[4096,1024] softmax, N(0,4) logits with an upper-triangular -inf mask."""
+    import shlo_hip
+    x, mask = causal_logits(oracle, 4096, 1024)
+    want = oracle.soft_max(x)
+    text = custom_call_module("ggml.soft_max", "scale = 0x3F800000 : f32", x.shape)
+    for compile in (True, False):
+        got = run(text, [x], compile=compile)[0]
+        assert same_bits(got, want), compile
+        assert np.all(got[mask] == 0) and not np.any(np.signbit(got[mask]))
+    got = run(text, [x], faults=shlo_hip.fault_bits("soft_max_float_sum"))[0]
+    assert not same_bits(got, want)
+
+
+@pytest.mark.parametrize("cols", [4, 16, 352, 512, 1020, 4096])
+def test_softmax_row_lengths(oracle, cols):
+    x, _ = oracle.fill_normal(11, 8.0, 64 * cols)
+    x = x.reshape(64, cols)
+    want = oracle.soft_max(x)
+    got = run(custom_call_module("ggml.soft_max", "scale = 0x3F800000 : f32", x.shape), [x])[0]
+    assert same_bits(got, want)
+
+
+def test_softmax_scale_attribute(oracle):
+    x, _ = oracle.fill_normal(12, 8.0, 32 * 256)
+    x = x.reshape(32, 256)
+    want = oracle.soft_max(x, scale=0.125)
+    got = run(custom_call_module("ggml.soft_max", "scale = 0x3E000000 : f32", x.shape), [x])[0]
+    assert same_bits(got, want)
+
+
+def test_gelu_config2b(oracle):
+    """erf-GELU over 64 Mi f32 ~ N(0,3): eager == graph on everything, and
+    against the oracle on a 1 Mi prefix and a strided 1 Mi sample."""
+    import shlo_hip
+    n = 64 << 20
+    x = shlo_hip.fill_random((n,), 8, 1, 3.0)
+    text = custom_call_module("ggml.gelu_erf", "", (n,))
+    m = shlo_hip.Module(text)
+    g = m.prepare(0, True).call([x])[0]
+    e = m.prepare(0, False).call([x])[0]
+    assert shlo_hip.count_nonzero(shlo_hip.binary("ne", shlo_hip.view(g, shlo_hip.U32),
+                                                  shlo_hip.view(e, shlo_hip.U32))) == 0
+    xs = x.numpy()
+    gs = g.numpy()
+    for sl in (slice(0, 1 << 20), slice(17, n, 64)):
+        want = oracle.gelu_erf(xs[sl])
+        assert same_bits(gs[sl], want)
+    f = m.prepare(shlo_hip.fault_bits("gelu_tanh"), True).call([x])[0].numpy()
+    assert not same_bits(f[:1 << 20], gs[:1 << 20])
+
+
+def test_gelu_special_values(oracle):
+    specials = np.array([0.0, -0.0, np.inf, -np.inf, 1e-45, -1e-45, 1e-38, 3.0, -3.0, 5.5, -5.5, 87.0, -87.0,
+                         3.4028235e38, -3.4028235e38], np.float32)
+    nan = np.array([0x7FC00000, 0x7F800001, 0xFFC01234, 0x7FBFFFFF], np.uint32).view(np.float32)
+    x = np.concatenate([specials, nan, np.zeros(1, np.float32)])
+    want = oracle.gelu_erf(x)
+    got = run(custom_call_module("ggml.gelu_erf", "", x.shape), [x])[0]
+    assert same_bits(got, want)
+
+
+def test_norm_and_silu_shapes(oracle):
+    import shlo_hip
+    for cols in (37, 512, 1024):
+        x, _ = oracle.fill_normal(5, 3.0, 96 * cols)
+        x = x.reshape(96, cols)
+        got = run(custom_call_module("ggml.norm", "eps = 0x3727C5AC : f32", x.shape), [x])[0]
+        assert same_bits(got, oracle.norm(x))
+    x, _ = oracle.fill_normal(9, 12.0, 64 * 1024)
+    x = x.reshape(64, 1024)
+    got = run(custom_call_module("ggml.silu", "", x.shape), [x])[0]
+    assert same_bits(got, oracle.silu(x))
+
+
+def test_random_fill_matches_oracle_stream(oracle):
+    import shlo_hip
+    u = shlo_hip.fill_random((1000,), 1, 0, 1.0).numpy()
+    assert same_bits(u, oracle.fill_unif(1, 1.0, 1000)[0])
+    v = shlo_hip.fill_random((1000,), 5, 1, 3.0).numpy()
+    assert same_bits(v, oracle.fill_normal(5, 3.0, 1000)[0])
+    w = shlo_hip.fill_random((500,), 5, 1, 3.0, skip=12 * 500).numpy()
+    _, st = oracle.fill_normal(5, 3.0, 500)
+    assert same_bits(w, oracle.fill_normal(5, 3.0, 500, state=st)[0])
