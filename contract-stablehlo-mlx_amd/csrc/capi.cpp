@@ -467,6 +467,30 @@ int shlo_timer_stop(float *ms) {
   });
 }
 
+int shlo_time_apply(shlo_fn *f, const shlo_arr *const *inputs, size_t nin, int reps, float *ms) {
+  return guard("time_apply", [&] {
+    need(f, "fn");
+    need(ms, "ms");
+    if (reps < 1) shlo::fail("reps must be >= 1");
+    std::vector<shlo::ArrayP> in;
+    for (size_t i = 0; i < nin; i++) in.push_back(A(inputs[i]));
+    (void)shlo::apply_fn(f->f, in);  // trace/instantiate outside the timed region
+    SHLO_HIP(hipStreamSynchronize(shlo::stream()));
+    hipEvent_t e0, e1;
+    SHLO_HIP(hipEventCreate(&e0));
+    SHLO_HIP(hipEventCreate(&e1));
+    SHLO_HIP(hipEventRecord(e0, shlo::stream()));
+    for (int r = 0; r < reps; r++) (void)shlo::apply_fn(f->f, in);
+    SHLO_HIP(hipEventRecord(e1, shlo::stream()));
+    SHLO_HIP(hipEventSynchronize(e1));
+    float t = 0;
+    SHLO_HIP(hipEventElapsedTime(&t, e0, e1));
+    (void)hipEventDestroy(e0);
+    (void)hipEventDestroy(e1);
+    *ms = t / (float)reps;
+  });
+}
+
 int shlo_device_info(char *name, size_t cap, int *cus, uint64_t *pool_bytes) {
   return guard("device_info", [&] {
     const hipDeviceProp_t &p = shlo::device_props();

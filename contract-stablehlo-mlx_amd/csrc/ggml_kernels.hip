@@ -92,6 +92,181 @@ __global__ void __launch_bounds__(256) dot_ggml_simple(int64_t n_out, int64_t N,
   }
 }
 
+// ---- dot_general on the matrix cores ------------------------------------------------
+//
+// ggml_vec_dot_f32 keeps 16 accumulators per output, accumulator j taking
+// fma(w[16b+j], x[16b+j], acc_j) over the blocks b in order.  Each chain is
+// an ordinary GEMM over the k = j (mod 16) slice, so it maps onto
+// v_mfma_f32_32x32x1_2b_f32: per instruction every output of two 32x32 blocks
+// gets exactly one fused multiply-add, acc = fma(a_i, b_j, acc), with one
+// rounding (checked bit for bit against fmaf, subnormals included).  Block 0
+// of instruction q carries residue q, block 1 residue q + 8, so a wave holds
+// all 16 chains of its 32x32 outputs in 8 accumulator sets (256 registers).
+// After the last block the fixed GGML_F32x4_REDUCE / vaddvq_f32 tree and the
+// serial tail run per output, exactly as in dot_finish.
+//
+// Workgroup: 4 waves on a 64 (n) x 64 (m) output tile; operands staged in LDS
+// as [row][k] (row stride KC + 4 floats), KC = 64 (four k-blocks) per stage,
+// double-buffered, the next stage prefetched into registers while the matrix
+// cores work on the current one.
+
+typedef float v32f __attribute__((ext_vector_type(32)));
+
+constexpr int kMT = 64;        // tile rows (n) and columns (m)
+constexpr int kKC = 64;        // k per stage
+constexpr int kLS = kKC + 4;   // LDS row stride (floats)
+
+// How an operand tile is loaded: kLoadRowVec = rows contiguous in k (sk == 1),
+// float4 along k; kLoadColVec = free dim contiguous (sf == 1), float4 along the
+// free dim, transposed into LDS; kLoadScalar = any strides.
+enum { kLoadRowVec = 0, kLoadColVec = 1, kLoadScalar = 2 };
+
+struct MfmaOperand {
+  const float *p;
+  int64_t sb, sf, sk;
+  int64_t rows;  // N or M
+};
+
+// Stage s of one operand into registers: 4096 floats per tile, 16 per thread.
+template <int LOAD>
+__device__ __forceinline__ void mfma_fetch(const MfmaOperand &o, int64_t b, int64_t r0, int s, int nb, float4 (&reg)[4]) {
+  const int t = threadIdx.x;
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const int f = t + 256 * i;
+    if (LOAD == kLoadColVec) {
+      const int kr = f / 16, rq = (f % 16) * 4;
+      const int k = s * kKC + kr;
+      int64_t row = r0 + rq;
+      if (row > o.rows - 4) row = o.rows - 4;  // stays in bounds; those outputs are discarded
+      if (k / 16 < nb) reg[i] = ld4(o.p + b * o.sb + row + (int64_t)k * o.sk);
+    } else {
+      const int row_l = f / 16, kq = (f % 16) * 4;
+      const int k = s * kKC + kq;
+      int64_t row = r0 + row_l;
+      if (row > o.rows - 1) row = o.rows - 1;
+      if (k / 16 < nb) {
+        const float *q = o.p + b * o.sb + row * o.sf;
+        if (LOAD == kLoadRowVec) {
+          reg[i] = ld4(q + k);
+        } else {
+          reg[i] = make_float4(q[(int64_t)k * o.sk], q[(int64_t)(k + 1) * o.sk], q[(int64_t)(k + 2) * o.sk],
+                               q[(int64_t)(k + 3) * o.sk]);
+        }
+      }
+    }
+  }
+}
+
+template <int LOAD>
+__device__ __forceinline__ void mfma_stash(float *lds, const float4 (&reg)[4]) {
+  const int t = threadIdx.x;
+#pragma unroll
+  for (int i = 0; i < 4; i++) {
+    const int f = t + 256 * i;
+    if (LOAD == kLoadColVec) {
+      const int kr = f / 16, rq = (f % 16) * 4;
+      lds[(rq + 0) * kLS + kr] = reg[i].x;
+      lds[(rq + 1) * kLS + kr] = reg[i].y;
+      lds[(rq + 2) * kLS + kr] = reg[i].z;
+      lds[(rq + 3) * kLS + kr] = reg[i].w;
+    } else {
+      const int row_l = f / 16, kq = (f % 16) * 4;
+      st4(lds + row_l * kLS + kq, reg[i]);
+    }
+  }
+}
+
+template <int LX, int LW>
+__global__ void __launch_bounds__(256) dot_mfma_k(MfmaOperand X, MfmaOperand W, int64_t N, int64_t M, int64_t K,
+                                                  int tail, int tiles_m, float *__restrict__ Y) {
+  __shared__ float lds[2][2][kMT * kLS];  // [buffer][operand: 0 = lhs rows n, 1 = rhs rows m]
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int wn = wave >> 1, wm = wave & 1;
+  const int64_t b = blockIdx.y;
+  const int64_t n0 = (int64_t)(blockIdx.x / tiles_m) * kMT, m0 = (int64_t)(blockIdx.x % tiles_m) * kMT;
+  const int64_t np = K & ~(int64_t)15;
+  const int nb = (int)(np / 16);
+  const int nst = (nb + kKC / 16 - 1) / (kKC / 16);
+
+  v32f acc[8];
+#pragma unroll
+  for (int q = 0; q < 8; q++)
+#pragma unroll
+    for (int r = 0; r < 32; r++) acc[q][r] = 0.0f;
+
+  float4 rx[4], rw[4];
+  if (nst > 0) {
+    mfma_fetch<LX>(X, b, n0, 0, nb, rx);
+    mfma_fetch<LW>(W, b, m0, 0, nb, rw);
+    mfma_stash<LX>(lds[0][0], rx);
+    mfma_stash<LW>(lds[0][1], rw);
+  }
+  __syncthreads();
+  const int h = lane >> 5, li = lane & 31;
+  for (int s = 0; s < nst; s++) {
+    const int buf = s & 1;
+    if (s + 1 < nst) {
+      mfma_fetch<LX>(X, b, n0, s + 1, nb, rx);
+      mfma_fetch<LW>(W, b, m0, s + 1, nb, rw);
+    }
+    const float *xs = lds[buf][0] + (wn * 32 + li) * kLS + 8 * h;
+    const float *ws = lds[buf][1] + (wm * 32 + li) * kLS + 8 * h;
+    const int blocks = min(kKC / 16, nb - s * (kKC / 16));
+    for (int blk = 0; blk < blocks; blk++) {
+      const float4 a0 = ld4(xs + 16 * blk), a1 = ld4(xs + 16 * blk + 4);
+      const float4 b0 = ld4(ws + 16 * blk), b1 = ld4(ws + 16 * blk + 4);
+      acc[0] = __builtin_amdgcn_mfma_f32_32x32x1f32(a0.x, b0.x, acc[0], 0, 0, 0);
+      acc[1] = __builtin_amdgcn_mfma_f32_32x32x1f32(a0.y, b0.y, acc[1], 0, 0, 0);
+      acc[2] = __builtin_amdgcn_mfma_f32_32x32x1f32(a0.z, b0.z, acc[2], 0, 0, 0);
+      acc[3] = __builtin_amdgcn_mfma_f32_32x32x1f32(a0.w, b0.w, acc[3], 0, 0, 0);
+      acc[4] = __builtin_amdgcn_mfma_f32_32x32x1f32(a1.x, b1.x, acc[4], 0, 0, 0);
+      acc[5] = __builtin_amdgcn_mfma_f32_32x32x1f32(a1.y, b1.y, acc[5], 0, 0, 0);
+      acc[6] = __builtin_amdgcn_mfma_f32_32x32x1f32(a1.z, b1.z, acc[6], 0, 0, 0);
+      acc[7] = __builtin_amdgcn_mfma_f32_32x32x1f32(a1.w, b1.w, acc[7], 0, 0, 0);
+    }
+    if (s + 1 < nst) {
+      mfma_stash<LX>(lds[buf ^ 1][0], rx);
+      mfma_stash<LW>(lds[buf ^ 1][1], rw);
+    }
+    __syncthreads();
+  }
+
+  // Epilogue: register r of set q holds block r/16 (residue q + 8*(r/16)) of
+  // output row i = 8*((r%16)/4) + 4*h + r%4, column j = lane%32.
+#pragma unroll
+  for (int r = 0; r < 16; r++) {
+    float t8[8];
+#pragma unroll
+    for (int q = 0; q < 8; q++) t8[q] = acc[q][r] + acc[q][r + 16];   // sum[0]+=sum[2], sum[1]+=sum[3]
+    float u0 = t8[0] + t8[4], u1 = t8[1] + t8[5], u2 = t8[2] + t8[6], u3 = t8[3] + t8[7];  // sum[0]+=sum[1]
+    float sumf = (u0 + u1) + (u2 + u3);                                  // vaddvq_f32
+    const int64_t n = n0 + wn * 32 + 8 * (r / 4) + 4 * h + (r % 4);
+    const int64_t m = m0 + wm * 32 + li;
+    if (n < N && m < M) {
+      if (np < K) {
+        const float *xr = X.p + b * X.sb + n * X.sf;
+        const float *wr = W.p + b * W.sb + m * W.sf;
+        if (tail == kTailPinned) {
+          for (int64_t k = np; k < K; k++) {
+            const float p = wr[k * W.sk] * xr[k * X.sk];
+            sumf = sumf + p;
+          }
+        } else {
+          const int64_t tl = K - np;
+          const int64_t nq = tl >= 4 ? (tl & ~(int64_t)3) : 0;
+          for (int64_t k = np; k < np + nq; k++) {
+            const float p = wr[k * W.sk] * xr[k * X.sk];
+            sumf = sumf + p;
+          }
+          for (int64_t k = np + nq; k < K; k++) sumf = __builtin_fmaf(wr[k * W.sk], xr[k * X.sk], sumf);
+        }
+      }
+      Y[(b * N + n) * M + m] = sumf;
+    }
+  }
+}
+
 // ---- soft_max ---------------------------------------------------------------------
 
 // One wave per row.  Lane l owns the four-element groups g = l + 64j, loaded
@@ -323,6 +498,34 @@ ArrayP dot_ggml(const DotOperand &lhs, const DotOperand &rhs, int64_t B, int64_t
   float *Y = (float *)y->data();
   ArrayP kl = lhs.arr, kr = rhs.arr;
   const int64_t lb = lhs.sb, ln = lhs.sf, lk = lhs.sk, rb = rhs.sb, rm = rhs.sf, rk = rhs.sk;
+  if (tail != kTailPlain && B <= 65535) {
+    auto loader = [&](const float *p, int64_t sb, int64_t sf, int64_t sk, int64_t rows) {
+      const bool al = ((uintptr_t)p % 16) == 0 && (sb % 4 == 0 || B == 1);
+      if (al && sk == 1 && (sf % 4 == 0 || rows == 1)) return (int)kLoadRowVec;
+      if (al && sf == 1 && sk % 4 == 0 && rows % 4 == 0) return (int)kLoadColVec;
+      return (int)kLoadScalar;
+    };
+    const int lx = loader(L, lb, ln, lk, N), lw = loader(R, rb, rm, rk, M);
+    const MfmaOperand X{L, lb, ln, lk, N}, W{R, rb, rm, rk, M};
+    const int tiles_m = (int)((M + kMT - 1) / kMT);
+    const int64_t tiles = ((N + kMT - 1) / kMT) * tiles_m;
+    if (tiles > 0x7FFFFFFF) fail("dot_general: too many output tiles");
+    const dim3 grid((unsigned)tiles, (unsigned)B);
+    const int tl = tail;
+    launch([=](hipStream_t s) {
+      (void)kl, (void)kr;
+#define DOT_CASE(a, c)                                                                    \
+  if (lx == a && lw == c) {                                                               \
+    dot_mfma_k<a, c><<<grid, 256, 0, s>>>(X, W, N, M, K, tl, tiles_m, Y);                \
+    return;                                                                               \
+  }
+      DOT_CASE(kLoadRowVec, kLoadRowVec) DOT_CASE(kLoadRowVec, kLoadColVec) DOT_CASE(kLoadRowVec, kLoadScalar)
+      DOT_CASE(kLoadColVec, kLoadRowVec) DOT_CASE(kLoadColVec, kLoadColVec) DOT_CASE(kLoadColVec, kLoadScalar)
+      DOT_CASE(kLoadScalar, kLoadRowVec) DOT_CASE(kLoadScalar, kLoadColVec) DOT_CASE(kLoadScalar, kLoadScalar)
+#undef DOT_CASE
+    });
+    return y;
+  }
   const unsigned grid = grid_cap(n_out, 256, 1 << 20);
   launch([=](hipStream_t s) {
     (void)kl, (void)kr;

@@ -320,6 +320,13 @@ class Fn:
         """Exec.call: apply, then wait for the outputs."""
         return self._run(_lib.shlo_call, inputs)
 
+    def time(self, inputs, reps):
+        """Mean ms per apply over `reps` back-to-back applies (HIP events)."""
+        arr = (ctypes.c_void_p * max(len(inputs), 1))(*[x._h.value for x in inputs])
+        ms = ctypes.c_float()
+        _check(_lib.shlo_time_apply(self._h, arr, _SZ(len(inputs)), ctypes.c_int(reps), ctypes.byref(ms)))
+        return ms.value
+
 
 def compile_fn(pyfn, enable=True) -> Fn:
     """Mlx.compile: wrap a Python function of Arr lists (traced on first apply when enabled)."""

@@ -201,12 +201,19 @@ int shlo_get_flavor(void);
  * `seed` and skips `skip` draws first. */
 int shlo_fill_random(const int64_t *shape, size_t rank, uint32_t seed, uint64_t skip, int dist, double param,
                      shlo_arr **out);
+/* The order-free checksum of 32-bit words used by the exhaustive erff fixture:
+ * sum over t of (w[t]+1)*(2(start+t)+1)*0x9E3779B97F4A7C15 mod 2^64. */
+int shlo_checksum_u32(const shlo_arr *a, uint64_t start_index, uint64_t *out);
 /* Wait for all queued work. */
 int shlo_sync(void);
 /* hipEvent timing on the executor's stream: start records an event, stop
  * records another, waits, and returns the milliseconds between them. */
 int shlo_timer_start(void);
 int shlo_timer_stop(float *ms);
+/* Apply `f` to the same inputs `reps` times back to back (outputs dropped at
+ * once) between two HIP events on the executor's stream; *ms = the mean
+ * milliseconds per apply.  Host call overhead stays outside the timed loop. */
+int shlo_time_apply(shlo_fn *f, const shlo_arr *const *inputs, size_t nin, int reps, float *ms);
 /* Device name, compute units and the bytes the array pool holds. */
 int shlo_device_info(char *name, size_t cap, int *cus, uint64_t *pool_bytes);
 /* The device address of an array's first element (for in-place interop). */
