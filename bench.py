@@ -119,7 +119,8 @@ def main():
                         ("dot_general_b16_1024x4096x4096", lambda: bench_dot(shlo, configs, 1024, 4096, 4096, 16, 2)),
                         ("dot_general_odd_257", lambda: bench_dot(shlo, configs, 257, 257, 257, 0, 20)),
                         ("erff_exhaustive_2^32", lambda: bench_erff(shlo)),
-                        ("attention_8x8x512x64", lambda: bench_attention(shlo, configs))):
+                        ("attention_8x8x512x64", lambda: bench_attention(shlo, configs)),
+                        ("denoiser_8L_d512_b32x256", lambda: bench_denoiser(shlo, configs))):
             try:
                 extra[key] = fn()
                 log(key, extra[key])
@@ -213,6 +214,17 @@ def bench_attention(shlo, configs, steps=5):
     ms = time_fn(shlo, f, [q, k, v, mask], steps, 1)
     fl = configs.attention_flops(B, H, S, D)
     return {"ms": round(ms, 4), "modules/s": round(1e3 / ms, 2), "dot GFLOP/s": round(fl / (ms * 1e-3) / 1e9, 1)}
+
+
+def bench_denoiser(shlo, configs, steps=10):
+    """one call of the compiled denoiser module (the
+    reference's shlo_mlx --repeat loop, Main.lean:83-87) per step."""
+    D = configs.Denoiser()
+    args = configs.denoiser_device_args(shlo, D)
+    f = shlo.Module(D.module()).prepare(0, True)
+    ms = time_fn(shlo, f, args, steps, 1)
+    return {"ms": round(ms, 3), "steps/s": round(1e3 / ms, 2),
+            "GFLOP/s": round(D.flops() / (ms * 1e-3) / 1e9, 1), "flop_per_step": D.flops()}
 
 
 def cpu_baseline():

@@ -220,3 +220,28 @@ def timestep_embedding(ts, d):
             out[b, 2 * i] = math.sin(w)
             out[b, 2 * i + 1] = math.cos(w)
     return out
+
+
+def denoiser_arg_seed(i):
+    """splitmix32 seed of the i-th denoiser argument (weights N(0, 0.02))."""
+    return 100 + i
+
+
+def denoiser_device_args(shlo, D, timesteps=None):
+    """The denoiser's arguments generated on the device (fill_random: the
+    splitmix32 Irwin-Hall normal); x ~ N(0,1), weights N(0,0.02), LayerNorm
+    gains 1 + N(0,0.02), temb from `timesteps` (default 10*b + 1)."""
+    import numpy as np
+    out = []
+    ts = timesteps if timesteps is not None else [10 * b + 1 for b in range(D.B)]
+    one = shlo.from_numpy(np.ones((D.d,), np.float32))
+    for i, (nm, shape, kind) in enumerate(D.args()):
+        if kind == "x":
+            out.append(shlo.fill_random(shape, 1000, 1, 1.0))
+        elif kind == "temb":
+            out.append(shlo.from_numpy(timestep_embedding(ts, D.d)))
+        elif kind == "g":
+            out.append(shlo.binary("add", one, shlo.fill_random(shape, denoiser_arg_seed(i), 1, 0.02)))
+        else:
+            out.append(shlo.fill_random(shape, denoiser_arg_seed(i), 1, 0.02))
+    return out

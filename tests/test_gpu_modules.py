@@ -81,3 +81,45 @@ def test_dot_config3_slices_vs_oracle(oracle):
             want = oracle.dot_general_bnk(arow[None], np.ascontiguousarray(bs.T)[None])[0]
             got = shlo_hip.slice_(y, (bi, n, 0), (bi + 1, n + 1, M), (1, 1, 1)).numpy()[0]
             assert same_bits(got, want), (bi, n)
+
+
+@pytest.mark.parametrize("dims", [dict(layers=2, d=128, heads=2, ffn=256, frames=32, feats=263, batch=2),
+                                  dict(layers=1, d=512, heads=8, ffn=2048, frames=64, feats=263, batch=2)])
+def test_denoiser_vs_oracle(oracle, dims):
+    """The denoiser module at reduced sizes against the oracle, graph and
+    eager, with planted faults in LayerNorm, GELU and dot_general."""
+    import denoiser_ref
+    import shlo_hip
+    from shlo_hip import configs
+    D = configs.Denoiser(**dims)
+    host = denoiser_ref.host_args(D)
+    dev = configs.denoiser_device_args(shlo_hip, D)
+    for h, g in zip(host, dev):
+        assert same_bits(g.numpy(), h)
+    want = denoiser_ref.forward(D, host)
+    m = shlo_hip.Module(D.module())
+    for compile in (True, False):
+        got = m.prepare(0, compile).call(dev)[0].numpy()
+        assert same_bits(got, want), compile
+    for fault in ("norm_gpu_ops", "gelu_tanh", "dot_plain"):
+        got = m.prepare(shlo_hip.fault_bits(fault), True).call(dev)[0].numpy()
+        assert not same_bits(got, want), fault
+
+
+def test_denoiser_config5_graph_equals_eager():
+    """The full config: 8 layers, d 512, 8 heads, FFN 2048, 256 frames x 263
+    features, batch 32; the compiled module repeated (--repeat) gives the same
+    bits every call, equal to the eager run."""
+    import shlo_hip
+    from shlo_hip import configs
+    D = configs.Denoiser()
+    dev = configs.denoiser_device_args(shlo_hip, D)
+    m = shlo_hip.Module(D.module())
+    e = m.prepare(0, False).call(dev)[0]
+    f = m.prepare(0, True)
+    for _ in range(3):
+        g = f.call(dev)[0]
+        assert shlo_hip.count_nonzero(shlo_hip.binary("ne", shlo_hip.view(g, shlo_hip.U32),
+                                                      shlo_hip.view(e, shlo_hip.U32))) == 0
+    y = e.numpy()
+    assert y.shape == (32, 256, 263) and np.all(np.isfinite(y))
