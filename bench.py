@@ -65,6 +65,8 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU oracle baseline")
     ap.add_argument("--no-extra", action="store_true", help="skip the other configs")
+    ap.add_argument("--only", choices=["hot", "gelu", "softmax", "dot3", "attention", "denoiser", "copy"],
+                    help="run one workload `--steps` times and print its timing (for profiling runs)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
@@ -75,6 +77,10 @@ def main():
 
     import shlo_hip as shlo
     from shlo_hip import configs
+
+    if args.only:
+        print(json.dumps(run_only(shlo, configs, args.only, args.steps, args.warmup)), flush=True)
+        return
 
     rows, cols, n = 4096, 1024, 64 << 20
     sm_bytes, ge_bytes = 8 * rows * cols, 8 * n
@@ -146,6 +152,46 @@ def main():
         "roofline": roofline, "cpu_baseline": cpu, "extra": extra,
     }
     print(json.dumps(line), flush=True)
+
+
+def run_only(shlo, configs, which, steps, warmup):
+    """One workload, `steps` timed applies of its compiled module (profiling runs)."""
+    rows, cols, n = 4096, 1024, 64 << 20
+    if which in ("hot", "softmax"):
+        logits = causal_logits_dev(shlo, rows, cols)
+    if which in ("hot", "gelu", "copy"):
+        x = shlo.fill_random((n,), 8, 1, 3.0)
+    if which == "hot":
+        f, ins, nbytes = shlo.Module(configs.hot_path_module(rows, cols, n)).prepare(0, True), [logits, x], 8 * (rows * cols + n)
+    elif which == "gelu":
+        f, ins, nbytes = shlo.Module(configs.unary_module("ggml.gelu_erf", "", (n,))).prepare(0, True), [x], 8 * n
+    elif which == "softmax":
+        f = shlo.Module(configs.unary_module("ggml.soft_max", configs.SOFTMAX_SCALE1, (rows, cols))).prepare(0, True)
+        ins, nbytes = [logits], 8 * rows * cols
+    elif which == "copy":
+        # calibration for the PMC byte counters: y = x + 0 over 64 Mi f32 reads
+        # 256 MiB and writes 256 MiB (the zero is one broadcast scalar)
+        zero = shlo.from_numpy(np.zeros((), np.float32))
+        f = shlo.compile_fn(lambda a: [shlo.binary("add", a[0], shlo.broadcast(a[1], (n,)))], True)
+        ins, nbytes = [x, zero], 8 * n
+    elif which == "dot3":
+        a = shlo.fill_random((16, 1024, 4096), 1, 0, 1.0)
+        b = shlo.fill_random((16, 4096, 4096), 1, 0, 1.0, skip=16 * 1024 * 4096)
+        f, ins, nbytes = shlo.Module(configs.dot_module(1024, 4096, 4096, 16)).prepare(0, True), [a, b], 0
+    elif which == "attention":
+        B, H, S, D = 8, 8, 512, 64
+        ins = [shlo.fill_random((B, H, S, D), 41 + i, 1, 1.0) for i in range(3)]
+        ins.append(shlo.from_numpy(np.where(np.triu(np.ones((S, S), bool), 1), np.float32(-np.inf), np.float32(0))))
+        f, nbytes = shlo.Module(configs.attention_module(B, H, S, D)).prepare(0, True), 0
+    else:
+        D = configs.Denoiser()
+        ins = configs.denoiser_device_args(shlo, D)
+        f, nbytes = shlo.Module(D.module()).prepare(0, True), 0
+    ms = time_fn(shlo, f, ins, steps, warmup)
+    res = {"workload": which, "steps": steps, "ms_per_step": round(ms, 5)}
+    if nbytes:
+        res["GB/s"] = round(nbytes / (ms * 1e-3) / 1e9, 1)
+    return res
 
 
 def traffic_from_profile():

@@ -30,41 +30,6 @@ __host__ __device__ inline uint32_t f2u(float f) { return __builtin_bit_cast(uin
 __host__ __device__ inline float u2f(uint32_t u) { return __builtin_bit_cast(float, u); }
 __host__ __device__ inline uint64_t d2u(double d) { return __builtin_bit_cast(uint64_t, d); }
 
-// erf(|x|) in binary64 for |x| < kOneBits, non-NaN; `tab` is kPoly (global,
-// constant or LDS copy).  Sets *undecided when the binary32 rounding of the
-// result is not certain.
-__host__ __device__ inline double erf_abs_binary64(uint32_t ax, const double *tab, bool *undecided) {
-  const float a = u2f(ax);
-  const double A = (double)a;
-  double R;
-  if (ax < 0x3D800000u) {  // a < 1/16
-    const double t = A * A;
-    double s = kSmall[5];
-    s = __builtin_fma(s, t, kSmall[4]);
-    s = __builtin_fma(s, t, kSmall[3]);
-    s = __builtin_fma(s, t, kSmall[2]);
-    s = __builtin_fma(s, t, kSmall[1]);
-    s = __builtin_fma(s, t, kSmall[0]);
-    R = A * s;
-  } else {
-    const int i = (int)(a * 64.0f);              // exact scaling, a < 4
-    const double h = A - (double)(2 * i + 1) * 0x1p-7;  // exact
-    const double *p = tab + 6 * i;
-    double s = p[5];
-    s = __builtin_fma(s, h, p[4]);
-    s = __builtin_fma(s, h, p[3]);
-    s = __builtin_fma(s, h, p[2]);
-    s = __builtin_fma(s, h, p[1]);
-    s = __builtin_fma(s, h, p[0]);
-    R = s;
-  }
-  // The binary32 rounding of R is decided by R's low 29 fraction bits (for a
-  // normal binary32 result): undecided within 2^7 units of the midpoint 2^28.
-  const uint32_t low = (uint32_t)d2u(R) & 0x1FFFFFFFu;
-  *undecided = (uint32_t)(low - (0x10000000u - 0x80u)) < 0x100u;
-  return R;
-}
-
 // Binary search of the sorted exception list (|x| bits -> |erf| bits).
 __host__ __device__ inline uint32_t exception_lookup(uint32_t ax, uint32_t fallback) {
   int lo = 0, hi = kNumExceptions - 1;
@@ -78,22 +43,49 @@ __host__ __device__ inline uint32_t exception_lookup(uint32_t ax, uint32_t fallb
   return fallback;
 }
 
+// erf(|x|) as binary32 bits before the exception lookup and without the
+// |x| >= kOneBits saturation, branch-free.  One Horner evaluation serves both
+// ranges: row i = floor(64|x|) of `tab` holds, for i < 4 (|x| < 1/16), the
+// small-argument polynomial S in t = x^2 (R = |x|*S(t)), and otherwise the
+// interval polynomial in h = |x| - c_i (R = P_i(h)).  The index is clamped so
+// NaN, infinity and |x| >= 4 stay in range (their results are replaced by the
+// caller).  *undecided is set when R's binary32 rounding is not certain.
+__host__ __device__ inline uint32_t erf_abs_bits_fast(uint32_t ax, const double *tab, bool *undecided) {
+  const float a = u2f(ax);
+  const double A = (double)a;
+  const float a64 = a * 64.0f;                                              // exact scaling
+  const int i = (int)(a64 < (float)(kTab - 1) ? a64 : (float)(kTab - 1));  // NaN -> kTab-1
+  const bool small = ax < 0x3D800000u;                                      // |x| < 1/16, i < 4
+  const double v = small ? A * A : A - (double)(2 * i + 1) * 0x1p-7;       // both exact
+  const double *p = tab + 6 * i;
+  double q = p[5];
+  q = __builtin_fma(q, v, p[4]);
+  q = __builtin_fma(q, v, p[3]);
+  q = __builtin_fma(q, v, p[2]);
+  q = __builtin_fma(q, v, p[1]);
+  q = __builtin_fma(q, v, p[0]);
+  const double R = small ? A * q : q;
+  // The binary32 rounding of R is decided by R's low 29 fraction bits: it is
+  // undecided within 2^7 units of the midpoint 2^28 (R = +0 is never flagged).
+  const uint32_t low = (uint32_t)d2u(R) & 0x1FFFFFFFu;
+  *undecided = ax < kOneBits && (uint32_t)(low - (0x10000000u - 0x80u)) < 0x100u;
+  return f2u((float)R);
+}
+
+// The correctly rounded erf of x's magnitude as bits, from the fast bits and
+// the undecided flag: the exception lookup, then saturation to 1.
+__host__ __device__ inline uint32_t erf_abs_bits_finish(uint32_t ax, uint32_t r, bool undecided) {
+  if (undecided) r = exception_lookup(ax, r);
+  return ax >= kOneBits ? 0x3F800000u : r;
+}
+
 __host__ __device__ inline float erff_cr(float x, const double *tab) {
   const uint32_t ux = f2u(x);
   const uint32_t ax = ux & 0x7FFFFFFFu;
-  if (ax > 0x7F800000u) return x + x;  // NaN: the input, quieted
-  uint32_t r;
-  if (ax >= kOneBits) {
-    r = 0x3F800000u;
-  } else if (ax == 0) {
-    r = 0;
-  } else {
-    bool undecided;
-    const double R = erf_abs_binary64(ax, tab, &undecided);
-    r = f2u((float)R);
-    if (undecided) r = exception_lookup(ax, r);
-  }
-  return u2f(r | (ux & 0x80000000u));
+  bool undecided;
+  const uint32_t r = erf_abs_bits_finish(ax, erf_abs_bits_fast(ax, tab, &undecided), undecided);
+  const float y = u2f(r | (ux & 0x80000000u));
+  return ax > 0x7F800000u ? x + x : y;  // NaN: the input, quieted
 }
 
 }  // namespace erffk

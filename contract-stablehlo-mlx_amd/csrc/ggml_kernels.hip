@@ -269,31 +269,45 @@ __global__ void __launch_bounds__(256) dot_mfma_k(MfmaOperand X, MfmaOperand W, 
 
 // ---- soft_max ---------------------------------------------------------------------
 
-// One wave per row.  Lane l owns the four-element groups g = l + 64j, loaded
-// as float4 (coalesced).  The row maximum is a wave reduction (exact: max is
-// order-free on non-NaN data); each group's e = ggml_v_expf(x*sc - mx) stays in
-// registers; each group's vaddvq_f32 part goes to LDS, and lane 0 adds the
-// parts to a binary64 sum in group order (ggml_vec_soft_max_f32's order,
-// Shaders.lean:111-120).  inv = (float)(1.0/sum), then y = e*inv.
-template <int J>
-__global__ void __launch_bounds__(256) soft_max_k(int64_t rows, int cols, float sc, int float_sum,
-                                                  const float *__restrict__ X, float *__restrict__ Y) {
+// ggml soft_max.  Lane l of a row's wave owns the four-element groups
+// g = l + 64j, loaded as float4 (coalesced).  The row maximum is a wave
+// reduction (exact: max is order-free on non-NaN data, and a +0/-0 tie
+// cannot change any output since exp(x - (+0)) = exp(x - (-0))); each group's
+// e = ggml_v_expf(x*sc - mx) stays in registers; each group's vaddvq_f32
+// part is added to a binary64 sum in group order (ggml_vec_soft_max_f32,
+// Shaders.lean:111-120); inv = (float)(1.0/sum), then y = e*inv.
+//
+// A block of 4*RPW rows: wave w computes rows w, w+4, ... as above (coalesced
+// float4 loads, wave max, ggml_v_expf values kept in registers) and writes
+// each group's part to LDS, one padded row per row.  Then lane r of wave 0
+// runs row r's binary64 sum over the parts in group order, so one v_add_f64
+// advances 4*RPW rows and the parts come from LDS without bank conflicts;
+// the other waves wait at the barrier.  Finally every wave scales and stores.
+template <int J, int RPW>
+__global__ void __launch_bounds__(256) soft_max_rows_k(int64_t rows, int cols, float sc, int float_sum,
+                                                       const float *__restrict__ X, float *__restrict__ Y) {
   extern __shared__ float lds[];
+  constexpr int RB = 4 * RPW;
   const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
   const int G = cols / 4;
-  float *parts = lds + wave * ((G + 3) / 4 * 4 + 4);
-  for (int64_t row = blockIdx.x * (int64_t)(blockDim.x / kWave) + wave; row < rows;
-       row += (int64_t)gridDim.x * (blockDim.x / kWave)) {
+  const int PS = (G + 3) / 4 * 4 + 4;
+  float *parts = lds;
+  float *invs = lds + RB * PS;
+  const int64_t row0 = blockIdx.x * (int64_t)RB;
+  float4 e[RPW][J];
+#pragma unroll
+  for (int rr = 0; rr < RPW; rr++) {
+    const int lr = wave + 4 * rr;
+    const int64_t row = row0 + lr;
+    if (row >= rows) continue;
     const float *x = X + row * cols;
-    float *y = Y + row * cols;
-    float4 e[J];
     float mx = -__builtin_inff();
 #pragma unroll
     for (int j = 0; j < J; j++) {
       const int g = lane + kWave * j;
       if (g < G) {
-        e[j] = ld4(x + 4 * g);
-        const float w0 = e[j].x * sc, w1 = e[j].y * sc, w2 = e[j].z * sc, w3 = e[j].w * sc;
+        e[rr][j] = ld4(x + 4 * g);
+        const float w0 = e[rr][j].x * sc, w1 = e[rr][j].y * sc, w2 = e[rr][j].z * sc, w3 = e[rr][j].w * sc;
         mx = mx > w0 ? mx : w0;
         mx = mx > w1 ? mx : w1;
         mx = mx > w2 ? mx : w2;
@@ -309,42 +323,181 @@ __global__ void __launch_bounds__(256) soft_max_k(int64_t rows, int cols, float 
     for (int j = 0; j < J; j++) {
       const int g = lane + kWave * j;
       if (g < G) {
-        e[j].x = ggml_v_expf(e[j].x * sc - mx);
-        e[j].y = ggml_v_expf(e[j].y * sc - mx);
-        e[j].z = ggml_v_expf(e[j].z * sc - mx);
-        e[j].w = ggml_v_expf(e[j].w * sc - mx);
-        parts[g] = (e[j].x + e[j].y) + (e[j].z + e[j].w);
+        e[rr][j].x = ggml_v_expf(e[rr][j].x * sc - mx);
+        e[rr][j].y = ggml_v_expf(e[rr][j].y * sc - mx);
+        e[rr][j].z = ggml_v_expf(e[rr][j].z * sc - mx);
+        e[rr][j].w = ggml_v_expf(e[rr][j].w * sc - mx);
+        parts[lr * PS + g] = (e[rr][j].x + e[rr][j].y) + (e[rr][j].z + e[rr][j].w);
+      }
+    }
+  }
+  __syncthreads();
+  if (wave == 0 && lane < RB && row0 + lane < rows) {
+    const float *pr = parts + lane * PS;
+    float inv;
+    if (float_sum) {  // planted: the denominator summed in binary32 (Shaders.lean:120-122)
+      float fs = 0.0f;
+      for (int g = 0; g < G; g++) fs = fs + pr[g];
+      inv = 1.0f / fs;
+    } else {
+      double s = 0.0;
+      int g = 0;
+      for (; g + 4 <= G; g += 4) {
+        const float4 p = ld4(pr + g);
+        s = s + (double)p.x;
+        s = s + (double)p.y;
+        s = s + (double)p.z;
+        s = s + (double)p.w;
+      }
+      for (; g < G; g++) s = s + (double)pr[g];
+      inv = (float)(1.0 / s);
+    }
+    invs[lane] = inv;
+  }
+  __syncthreads();
+#pragma unroll
+  for (int rr = 0; rr < RPW; rr++) {
+    const int lr = wave + 4 * rr;
+    const int64_t row = row0 + lr;
+    if (row >= rows) continue;
+    const float inv = invs[lr];
+    float *y = Y + row * cols;
+#pragma unroll
+    for (int j = 0; j < J; j++) {
+      const int g = lane + kWave * j;
+      if (g < G) st4(y + 4 * g, make_float4(e[rr][j].x * inv, e[rr][j].y * inv, e[rr][j].z * inv, e[rr][j].w * inv));
+    }
+  }
+}
+
+// Doubles per row of parts in soft_max_pipe_k: even, so every row starts
+// 16-byte aligned for the double2 reads.
+__host__ __device__ inline int softmax_pipe_row_doubles(int G) { return (G + 1) / 2 * 2 + 2; }
+
+// Persistent, software-pipelined variant: each wave owns RPW rows at a time
+// (rows w*RPW .. w*RPW+RPW-1, then the same rows plus RPW*waves, ...).  While
+// the current rows are being exponentiated and summed, the next rows' loads are
+// already in flight.  Group parts are stored to the wave's own LDS region as
+// binary64 (converted by all lanes in parallel), and lane r runs row r's sum
+// in group order, so one v_add_f64 advances RPW rows and no block barrier is
+// needed.
+template <int J, int RPW>
+__global__ void __launch_bounds__(256) soft_max_pipe_k(int64_t rows, int cols, float sc, int float_sum,
+                                                       const float *__restrict__ X, float *__restrict__ Y) {
+  extern __shared__ double ldsd[];
+  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  const int G = cols / 4;
+  const int RS = softmax_pipe_row_doubles(G);
+  double *parts = ldsd + (size_t)wave * RPW * RS;
+  const int64_t gw = blockIdx.x * (int64_t)(blockDim.x / kWave) + wave;
+  const int64_t nw = (int64_t)gridDim.x * (blockDim.x / kWave);
+  float4 cur[RPW][J], nxt[RPW][J];
+  auto fetch = [&](int64_t r0, float4 (&dst)[RPW][J]) {
+#pragma unroll
+    for (int rr = 0; rr < RPW; rr++) {
+      const int64_t row = r0 + rr;
+      if (row >= rows) continue;
+      const float *x = X + row * cols;
+#pragma unroll
+      for (int j = 0; j < J; j++) {
+        const int g = lane + kWave * j;
+        if (g < G) dst[rr][j] = ld4(x + 4 * g);
+      }
+    }
+  };
+  int64_t r0 = gw * RPW;
+  if (r0 < rows) fetch(r0, cur);
+  for (; r0 < rows; r0 += nw * RPW) {
+    const int64_t n0 = r0 + nw * RPW;
+    if (n0 < rows) fetch(n0, nxt);
+#pragma unroll
+    for (int rr = 0; rr < RPW; rr++) {
+      if (r0 + rr >= rows) continue;
+      float mx = -__builtin_inff();
+#pragma unroll
+      for (int j = 0; j < J; j++) {
+        const int g = lane + kWave * j;
+        if (g < G) {
+          const float w0 = cur[rr][j].x * sc, w1 = cur[rr][j].y * sc, w2 = cur[rr][j].z * sc, w3 = cur[rr][j].w * sc;
+          mx = mx > w0 ? mx : w0;
+          mx = mx > w1 ? mx : w1;
+          mx = mx > w2 ? mx : w2;
+          mx = mx > w3 ? mx : w3;
+        }
+      }
+#pragma unroll
+      for (int o = 32; o > 0; o >>= 1) {
+        const float other = __shfl_xor(mx, o, kWave);
+        mx = mx > other ? mx : other;
+      }
+#pragma unroll
+      for (int j = 0; j < J; j++) {
+        const int g = lane + kWave * j;
+        if (g < G) {
+          cur[rr][j].x = ggml_v_expf(cur[rr][j].x * sc - mx);
+          cur[rr][j].y = ggml_v_expf(cur[rr][j].y * sc - mx);
+          cur[rr][j].z = ggml_v_expf(cur[rr][j].z * sc - mx);
+          cur[rr][j].w = ggml_v_expf(cur[rr][j].w * sc - mx);
+          const float part = (cur[rr][j].x + cur[rr][j].y) + (cur[rr][j].z + cur[rr][j].w);
+          if (float_sum) reinterpret_cast<float *>(parts + rr * RS)[g] = part;
+          else parts[rr * RS + g] = (double)part;
+        }
       }
     }
     wave_sync();
     float inv = 0.0f;
-    if (lane == 0) {
+    if (lane < RPW && r0 + lane < rows) {
       if (float_sum) {  // planted: the denominator summed in binary32 (Shaders.lean:120-122)
+        const float *pr = reinterpret_cast<const float *>(parts + lane * RS);
         float fs = 0.0f;
-        for (int g = 0; g < G; g++) fs = fs + parts[g];
+        for (int g = 0; g < G; g++) fs = fs + pr[g];
         inv = 1.0f / fs;
       } else {
+        const double *pr = parts + lane * RS;
         double s = 0.0;
         int g = 0;
         for (; g + 4 <= G; g += 4) {
-          const float4 p = ld4(parts + g);
-          s = s + (double)p.x;
-          s = s + (double)p.y;
-          s = s + (double)p.z;
-          s = s + (double)p.w;
+          const double2 a = *reinterpret_cast<const double2 *>(pr + g);
+          const double2 b = *reinterpret_cast<const double2 *>(pr + g + 2);
+          s = s + a.x;
+          s = s + a.y;
+          s = s + b.x;
+          s = s + b.y;
         }
-        for (; g < G; g++) s = s + (double)parts[g];
+        for (; g < G; g++) s = s + pr[g];
         inv = (float)(1.0 / s);
       }
     }
-    inv = __shfl(inv, 0, kWave);
 #pragma unroll
-    for (int j = 0; j < J; j++) {
-      const int g = lane + kWave * j;
-      if (g < G) st4(y + 4 * g, make_float4(e[j].x * inv, e[j].y * inv, e[j].z * inv, e[j].w * inv));
+    for (int rr = 0; rr < RPW; rr++) {
+      const float iv = __shfl(inv, rr, kWave);
+      const int64_t row = r0 + rr;
+      if (row >= rows) continue;
+      float *y = Y + row * cols;
+#pragma unroll
+      for (int j = 0; j < J; j++) {
+        const int g = lane + kWave * j;
+        if (g < G) st4(y + 4 * g, make_float4(cur[rr][j].x * iv, cur[rr][j].y * iv, cur[rr][j].z * iv, cur[rr][j].w * iv));
+      }
     }
     wave_sync();
+#pragma unroll
+    for (int rr = 0; rr < RPW; rr++)
+#pragma unroll
+      for (int j = 0; j < J; j++) cur[rr][j] = nxt[rr][j];
   }
+}
+
+int env_int(const char *name, int dflt) {
+  const char *s = getenv(name);
+  return s ? atoi(s) : dflt;
+}
+
+int softmax_rows_per_wave(int J) {
+  static const int env = env_int("SHLO_SOFTMAX_RPW", 0);
+  if (J > 4) return 1;
+  if (env == 1 || env == 2 || env == 4) return env;
+  return 2;
 }
 
 // ---- norm ---------------------------------------------------------------------------
@@ -447,16 +600,51 @@ __device__ __forceinline__ float gelu1(float x, const double *tab, int tanh_form
   return y;
 }
 
+// Four elements at once: the four erf evaluations share one (rarely taken)
+// branch into the exception table.  Same results as gelu1 element by element.
+__device__ __forceinline__ float4 gelu4(float4 v, const double *tab, int tanh_form) {
+  if (tanh_form)
+    return make_float4(gelu1(v.x, tab, 1), gelu1(v.y, tab, 1), gelu1(v.z, tab, 1), gelu1(v.w, tab, 1));
+  const float x[4] = {v.x, v.y, v.z, v.w};
+  uint32_t ux[4], ax[4], r[4];
+  bool u[4];
+#pragma unroll
+  for (int k = 0; k < 4; k++) {
+    ux[k] = f_bits(x[k] * bits_f(0x3F3504F3u));  // SQRT_2_INV
+    ax[k] = ux[k] & 0x7FFFFFFFu;
+    r[k] = erffk::erf_abs_bits_fast(ax[k], tab, &u[k]);
+  }
+  if (u[0] | u[1] | u[2] | u[3]) {
+#pragma unroll
+    for (int k = 0; k < 4; k++)
+      if (u[k]) r[k] = erffk::exception_lookup(ax[k], r[k]);
+  }
+  float y[4];
+#pragma unroll
+  for (int k = 0; k < 4; k++) {
+    r[k] = ax[k] >= erffk::kOneBits ? 0x3F800000u : r[k];
+    const float ev = bits_f(r[k] | (ux[k] & 0x80000000u));
+    y[k] = (0.5f * x[k]) * (1.0f + ev);
+    // A NaN input gives the input quieted, payload kept (Shaders.lean:196-199).
+    if ((f_bits(x[k]) & 0x7FFFFFFFu) > 0x7F800000u) y[k] = bits_f(f_bits(x[k]) | 0x00400000u);
+  }
+  return make_float4(y[0], y[1], y[2], y[3]);
+}
+
+// Two float4 per thread per iteration, both loads issued before the math.
 __global__ void __launch_bounds__(256) gelu_erf_k(int64_t n, int tanh_form, const float *__restrict__ X,
                                                   float *__restrict__ Y) {
   __shared__ double tab[kPolyWords];
   load_poly(tab);
   const int64_t n4 = n / 4;
-  for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n4; i += (int64_t)gridDim.x * blockDim.x) {
-    const float4 v = ld4(X + 4 * i);
-    st4(Y + 4 * i, make_float4(gelu1(v.x, tab, tanh_form), gelu1(v.y, tab, tanh_form), gelu1(v.z, tab, tanh_form),
-                               gelu1(v.w, tab, tanh_form)));
+  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+  int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
+  for (; i + stride < n4; i += 2 * stride) {
+    const float4 v0 = ld4(X + 4 * i), v1 = ld4(X + 4 * (i + stride));
+    st4(Y + 4 * i, gelu4(v0, tab, tanh_form));
+    st4(Y + 4 * (i + stride), gelu4(v1, tab, tanh_form));
   }
+  if (i < n4) st4(Y + 4 * i, gelu4(ld4(X + 4 * i), tab, tanh_form));
   for (int64_t i = 4 * n4 + blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
     Y[i] = gelu1(X[i], tab, tanh_form);
 }
@@ -567,23 +755,60 @@ ArrayP soft_max(const ArrayP &x0, int64_t rows, int64_t cols, uint32_t scale_bit
   if (rows == 0 || cols == 0) return y;
   const float sc = bits_f(scale_bits);
   const int J = (int)((cols / 4 + kWave - 1) / kWave);
-  const int lds = 4 * (int)((cols / 4 + 3) / 4 * 4 + 4) * (int)sizeof(float);
-  const unsigned grid = grid_cap(rows, 4, 1 << 20);
+  const int RPW = softmax_rows_per_wave(J);
   const float *px = (const float *)x->data();
   float *py = (float *)y->data();
   const int c = (int)cols;
   const int fs = float_sum ? 1 : 0;
   ArrayP kx = x;
+  static const int pipe_blocks = env_int("SHLO_SOFTMAX_PIPE", 0);
+  if (pipe_blocks > 0) {
+    const int64_t waves = (rows + RPW - 1) / RPW;
+    const unsigned grid = (unsigned)std::min<int64_t>((waves + 3) / 4, pipe_blocks);
+    const int lds = 4 * RPW * softmax_pipe_row_doubles((int)(cols / 4)) * (int)sizeof(double);
+    launch([=](hipStream_t s) {
+      (void)kx;
+#define SMP_CASE(n)                                                                                 \
+  case n:                                                                                           \
+    if (RPW == 4) soft_max_pipe_k<n, 4><<<grid, 256, lds, s>>>(rows, c, sc, fs, px, py);            \
+    else if (RPW == 2) soft_max_pipe_k<n, 2><<<grid, 256, lds, s>>>(rows, c, sc, fs, px, py);       \
+    else soft_max_pipe_k<n, 1><<<grid, 256, lds, s>>>(rows, c, sc, fs, px, py);                     \
+    break;
+#define SMP_CASE1(n) \
+  case n: soft_max_pipe_k<n, 1><<<grid, 256, lds, s>>>(rows, c, sc, fs, px, py); break;
+      switch (J) {
+        SMP_CASE(1) SMP_CASE(2) SMP_CASE(3) SMP_CASE(4) SMP_CASE1(5) SMP_CASE1(6) SMP_CASE1(7) SMP_CASE1(8)
+        SMP_CASE1(9) SMP_CASE1(10) SMP_CASE1(11) SMP_CASE1(12) SMP_CASE1(13) SMP_CASE1(14) SMP_CASE1(15)
+        SMP_CASE1(16)
+        default: break;
+      }
+#undef SMP_CASE
+#undef SMP_CASE1
+    });
+    return y;
+  }
+  const int PS = (int)((cols / 4 + 3) / 4 * 4 + 4);
+  const int lds = (4 * RPW * PS + 4 * RPW) * (int)sizeof(float);
+  const int64_t nblk = (rows + 4 * RPW - 1) / (4 * RPW);
+  if (nblk > 0x7FFFFFFF) fail("ggml.soft_max: too many rows");
+  const unsigned grid = (unsigned)nblk;
   launch([=](hipStream_t s) {
     (void)kx;
+#define SM_CASE(n)                                                                                  \
+  case n:                                                                                           \
+    if (RPW == 4) soft_max_rows_k<n, 4><<<grid, 256, lds, s>>>(rows, c, sc, fs, px, py);            \
+    else if (RPW == 2) soft_max_rows_k<n, 2><<<grid, 256, lds, s>>>(rows, c, sc, fs, px, py);       \
+    else soft_max_rows_k<n, 1><<<grid, 256, lds, s>>>(rows, c, sc, fs, px, py);                     \
+    break;
+#define SM_CASE1(n) \
+  case n: soft_max_rows_k<n, 1><<<grid, 256, lds, s>>>(rows, c, sc, fs, px, py); break;
     switch (J) {
-#define SM_CASE(n) \
-  case n: soft_max_k<n><<<grid, 256, lds, s>>>(rows, c, sc, fs, px, py); break;
-      SM_CASE(1) SM_CASE(2) SM_CASE(3) SM_CASE(4) SM_CASE(5) SM_CASE(6) SM_CASE(7) SM_CASE(8)
-      SM_CASE(9) SM_CASE(10) SM_CASE(11) SM_CASE(12) SM_CASE(13) SM_CASE(14) SM_CASE(15) SM_CASE(16)
-#undef SM_CASE
+      SM_CASE(1) SM_CASE(2) SM_CASE(3) SM_CASE(4) SM_CASE1(5) SM_CASE1(6) SM_CASE1(7) SM_CASE1(8)
+      SM_CASE1(9) SM_CASE1(10) SM_CASE1(11) SM_CASE1(12) SM_CASE1(13) SM_CASE1(14) SM_CASE1(15) SM_CASE1(16)
       default: break;
     }
+#undef SM_CASE
+#undef SM_CASE1
   });
   return y;
 }
