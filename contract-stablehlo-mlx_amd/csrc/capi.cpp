@@ -428,6 +428,14 @@ int shlo_set_flavor(int flavor) {
 }
 int shlo_get_flavor(void) { return shlo::default_dot_tail(); }
 
+int shlo_set_graph_min_ops(int n, int *prev) {
+  return guard("graph_min_ops", [&] {
+    if (n < 1) shlo::fail("graph_min_ops: n must be at least 1");
+    const size_t old = shlo::set_graph_min_ops((size_t)n);
+    if (prev) *prev = (int)old;
+  });
+}
+
 int shlo_fill_random(const int64_t *shape, size_t rank, uint32_t seed, uint64_t skip, int dist, double param,
                      shlo_arr **out) {
   return guard("fill_random", [&] {

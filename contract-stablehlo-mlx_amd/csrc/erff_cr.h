@@ -6,11 +6,11 @@
 // libsystem_m erff is closed code and not reproduced here.  A correctly rounded
 // function is fixed by the mathematics, so this routine is our own:
 //
-//   a = |x| in binary64;  R = a*S(a^2) (a < 1/16)  or  P_i(a - c_i) (table);
-//   y = RN_binary32(R), sign restored.
+//   a = min(|x|, 255/64);  R = a * Q_i(64 a - i), i = floor(64 a)  (table,
+//   binary64);  y = RN_binary32(R), sign restored.
 //
-// The tables (erff_tables.h) bound |R - erf(a)| by 2^-49.3 relative.  When R
-// lies within 2^7 binary64 units (2^-45 relative) of a binary32 rounding
+// The tables (erff_tables.h) bound |Q_i - erf(a)/a| by 2^-51.8 relative.  When
+// R lies within 2^5 binary64 units (2^-47 relative) of a binary32 rounding
 // boundary the rounding is undecided, and the input's correctly rounded value
 // is looked up in erff_exceptions.h, which lists every such input.  The whole
 // function is checked on all 2^32 inputs against MPFR.
@@ -43,48 +43,53 @@ __host__ __device__ inline uint32_t exception_lookup(uint32_t ax, uint32_t fallb
   return fallback;
 }
 
-// erf(|x|) as binary32 bits before the exception lookup and without the
-// |x| >= kOneBits saturation, branch-free.  One Horner evaluation serves both
-// ranges: row i = floor(64|x|) of `tab` holds, for i < 4 (|x| < 1/16), the
-// small-argument polynomial S in t = x^2 (R = |x|*S(t)), and otherwise the
-// interval polynomial in h = |x| - c_i (R = P_i(h)).  The index is clamped so
-// NaN, infinity and |x| >= 4 stay in range (their results are replaced by the
-// caller).  *undecided is set when R's binary32 rounding is not certain.
-__host__ __device__ inline uint32_t erf_abs_bits_fast(uint32_t ax, const double *tab, bool *undecided) {
-  const float a = u2f(ax);
-  const double A = (double)a;
-  const float a64 = a * 64.0f;                                              // exact scaling
-  const int i = (int)(a64 < (float)(kTab - 1) ? a64 : (float)(kTab - 1));  // NaN -> kTab-1
-  const bool small = ax < 0x3D800000u;                                      // |x| < 1/16, i < 4
-  const double v = small ? A * A : A - (double)(2 * i + 1) * 0x1p-7;       // both exact
+// Inputs are clamped to kClampA = 255/64, the start of the last interval:
+// erf(kClampA) rounds to 1, as erf of every larger input (and infinity) does.
+constexpr float kClampA = 3.984375f;
+constexpr uint32_t kClampBits = 0x407F0000u;
+
+// R ~ erf(min(a, kClampA)) in binary64 for a = |x| >= 0 or a quiet NaN (which
+// clamps too: v_min_f32 and fminf return the number), branch-free:
+// R = a * Q_i(u) with i = floor(64 a) and u = 64 a - i (exact in binary32),
+// Q_i row i of `tab`.
+__host__ __device__ inline double erf_abs_R(float a, const double *tab) {
+  const float ac = __builtin_fminf(a, kClampA);
+  const float a64 = ac * 64.0f;  // exact scaling, <= 255
+  const unsigned i = (unsigned)(int)a64 & (unsigned)(kTab - 1);
+#if defined(__HIP_DEVICE_COMPILE__)
+  const float uf = __builtin_amdgcn_fractf(a64);  // a64 - floor(a64), exact for a64 >= 0
+#else
+  const float uf = a64 - (float)(int)a64;  // exact (Sterbenz for a64 >= 1)
+#endif
+  const double u = (double)uf;
   const double *p = tab + 6 * i;
   double q = p[5];
-  q = __builtin_fma(q, v, p[4]);
-  q = __builtin_fma(q, v, p[3]);
-  q = __builtin_fma(q, v, p[2]);
-  q = __builtin_fma(q, v, p[1]);
-  q = __builtin_fma(q, v, p[0]);
-  const double R = small ? A * q : q;
-  // The binary32 rounding of R is decided by R's low 29 fraction bits: it is
-  // undecided within 2^7 units of the midpoint 2^28 (R = +0 is never flagged).
-  const uint32_t low = (uint32_t)d2u(R) & 0x1FFFFFFFu;
-  *undecided = ax < kOneBits && (uint32_t)(low - (0x10000000u - 0x80u)) < 0x100u;
-  return f2u((float)R);
+  q = __builtin_fma(q, u, p[4]);
+  q = __builtin_fma(q, u, p[3]);
+  q = __builtin_fma(q, u, p[2]);
+  q = __builtin_fma(q, u, p[1]);
+  q = __builtin_fma(q, u, p[0]);
+  return (double)ac * q;
 }
 
-// The correctly rounded erf of x's magnitude as bits, from the fast bits and
-// the undecided flag: the exception lookup, then saturation to 1.
-__host__ __device__ inline uint32_t erf_abs_bits_finish(uint32_t ax, uint32_t r, bool undecided) {
-  if (undecided) r = exception_lookup(ax, r);
-  return ax >= kOneBits ? 0x3F800000u : r;
+// The binary32 rounding of R is decided by R's low 29 fraction bits: it is
+// undecided within 2^5 units of the midpoint 2^28.  undecided_distance(R) < 64
+// exactly when R is undecided (R = +0 never is).
+__host__ __device__ inline uint32_t undecided_distance(double R) {
+  return ((uint32_t)d2u(R) & 0x1FFFFFFFu) - (0x10000000u - 0x20u);
+}
+
+// The correctly rounded erf of |x| as bits, for |x|'s bits ax (NaN excluded).
+__host__ __device__ inline uint32_t erf_abs_bits(uint32_t ax, const double *tab) {
+  const double R = erf_abs_R(u2f(ax), tab);
+  const uint32_t r = f2u((float)R);
+  return undecided_distance(R) < 0x40u ? exception_lookup(ax, r) : r;
 }
 
 __host__ __device__ inline float erff_cr(float x, const double *tab) {
   const uint32_t ux = f2u(x);
   const uint32_t ax = ux & 0x7FFFFFFFu;
-  bool undecided;
-  const uint32_t r = erf_abs_bits_finish(ax, erf_abs_bits_fast(ax, tab, &undecided), undecided);
-  const float y = u2f(r | (ux & 0x80000000u));
+  const float y = u2f(erf_abs_bits(ax, tab) | (ux & 0x80000000u));
   return ax > 0x7F800000u ? x + x : y;  // NaN: the input, quieted
 }
 

@@ -5,6 +5,8 @@
 // eager and graph-replayed runs give identical bits.
 #include <hip/hip_runtime.h>
 
+#include <type_traits>
+
 #include "erff_cr.h"
 #include "ggml_expf.h"
 #include "ops.h"
@@ -269,6 +271,41 @@ __global__ void __launch_bounds__(256) dot_mfma_k(MfmaOperand X, MfmaOperand W, 
 
 // ---- soft_max ---------------------------------------------------------------------
 
+// The binary64 sum s = ((0 + p[0]) + p[1]) + ... + p[n-1] of n parts in LDS
+// (16-byte aligned), strictly in order.  The reads run one batch of 16 ahead
+// of the dependent adds, so the chain waits on the adds and not on the LDS.
+template <typename T>
+__device__ __forceinline__ double chain_sum_f64(const T *p, int n) {
+  constexpr int kB = 16;
+  constexpr int kV = 16 / (int)sizeof(T);  // elements per 16-byte read
+  using V = typename std::conditional<sizeof(T) == 4, float4, double2>::type;
+  double s = 0.0;
+  V cur[kB / kV], nxt[kB / kV];
+  const int nb = n / kB;
+  if (nb > 0) {
+#pragma unroll
+    for (int k = 0; k < kB / kV; k++) cur[k] = reinterpret_cast<const V *>(p)[k];
+  }
+#pragma unroll 1
+  for (int b = 0; b < nb; b++) {
+    // Unconditional (the last batch re-reads itself), so no branch makes the
+    // compiler wait for these reads before the adds below.
+    const T *q = p + (b + 1 < nb ? b + 1 : b) * kB;
+#pragma unroll
+    for (int k = 0; k < kB / kV; k++) nxt[k] = reinterpret_cast<const V *>(q)[k];
+#pragma unroll
+    for (int k = 0; k < kB / kV; k++) {
+      const T *e = reinterpret_cast<const T *>(&cur[k]);
+#pragma unroll
+      for (int m = 0; m < kV; m++) s = s + (double)e[m];
+    }
+#pragma unroll
+    for (int k = 0; k < kB / kV; k++) cur[k] = nxt[k];
+  }
+  for (int g = nb * kB; g < n; g++) s = s + (double)p[g];
+  return s;
+}
+
 // ggml soft_max.  Lane l of a row's wave owns the four-element groups
 // g = l + 64j, loaded as float4 (coalesced).  The row maximum is a wave
 // reduction (exact: max is order-free on non-NaN data, and a +0/-0 tie
@@ -340,17 +377,7 @@ __global__ void __launch_bounds__(256) soft_max_rows_k(int64_t rows, int cols, f
       for (int g = 0; g < G; g++) fs = fs + pr[g];
       inv = 1.0f / fs;
     } else {
-      double s = 0.0;
-      int g = 0;
-      for (; g + 4 <= G; g += 4) {
-        const float4 p = ld4(pr + g);
-        s = s + (double)p.x;
-        s = s + (double)p.y;
-        s = s + (double)p.z;
-        s = s + (double)p.w;
-      }
-      for (; g < G; g++) s = s + (double)pr[g];
-      inv = (float)(1.0 / s);
+      inv = (float)(1.0 / chain_sum_f64(pr, G));
     }
     invs[lane] = inv;
   }
@@ -453,19 +480,7 @@ __global__ void __launch_bounds__(256) soft_max_pipe_k(int64_t rows, int cols, f
         for (int g = 0; g < G; g++) fs = fs + pr[g];
         inv = 1.0f / fs;
       } else {
-        const double *pr = parts + lane * RS;
-        double s = 0.0;
-        int g = 0;
-        for (; g + 4 <= G; g += 4) {
-          const double2 a = *reinterpret_cast<const double2 *>(pr + g);
-          const double2 b = *reinterpret_cast<const double2 *>(pr + g + 2);
-          s = s + a.x;
-          s = s + a.y;
-          s = s + b.x;
-          s = s + b.y;
-        }
-        for (; g < G; g++) s = s + pr[g];
-        inv = (float)(1.0 / s);
+        inv = (float)(1.0 / chain_sum_f64(parts + lane * RS, G));
       }
     }
 #pragma unroll
@@ -497,7 +512,7 @@ int softmax_rows_per_wave(int J) {
   static const int env = env_int("SHLO_SOFTMAX_RPW", 0);
   if (J > 4) return 1;
   if (env == 1 || env == 2 || env == 4) return env;
-  return 2;
+  return 1;
 }
 
 // ---- norm ---------------------------------------------------------------------------
@@ -583,14 +598,35 @@ __global__ void __launch_bounds__(256) silu_k(int64_t n, int gpu_ops, const floa
 
 constexpr int kPolyWords = erffk::kTab * 6;
 
+// Stages the coefficient table in LDS (16-byte loads; the table is read from
+// L2 after the first blocks).
 __device__ __forceinline__ void load_poly(double *tab) {
-  for (int i = threadIdx.x; i < kPolyWords; i += blockDim.x) tab[i] = (&erffk::kPoly[0][0])[i];
+  const double2 *src = reinterpret_cast<const double2 *>(&erffk::kPoly[0][0]);
+  for (int i = threadIdx.x; i < kPolyWords / 2; i += blockDim.x) reinterpret_cast<double2 *>(tab)[i] = src[i];
   __syncthreads();
 }
 
-__device__ __forceinline__ float gelu1(float x, const double *tab, int tanh_form) {
+// Streaming loads and stores: each byte of a unary map's operands is touched
+// once, so they bypass cache allocation (the `nt` bit).
+__device__ __forceinline__ float4 ld4_nt(const float *p) {
+  float4 v;
+  v.x = __builtin_nontemporal_load(p);
+  v.y = __builtin_nontemporal_load(p + 1);
+  v.z = __builtin_nontemporal_load(p + 2);
+  v.w = __builtin_nontemporal_load(p + 3);
+  return v;
+}
+__device__ __forceinline__ void st4_nt(float *p, float4 v) {
+  __builtin_nontemporal_store(v.x, p);
+  __builtin_nontemporal_store(v.y, p + 1);
+  __builtin_nontemporal_store(v.z, p + 2);
+  __builtin_nontemporal_store(v.w, p + 3);
+}
+
+template <int TANH>
+__device__ __forceinline__ float gelu1(float x, const double *tab) {
   float ev;
-  if (tanh_form)  // planted: the tanh form of GELU (Shaders.lean:192-194)
+  if (TANH)  // planted: the tanh form of GELU (Shaders.lean:192-194)
     ev = tanhf(bits_f(0x3F4C422Au) * x * (1.0f + bits_f(0x3D372713u) * x * x));
   else
     ev = erffk::erff_cr(x * bits_f(0x3F3504F3u), tab);  // SQRT_2_INV
@@ -600,53 +636,73 @@ __device__ __forceinline__ float gelu1(float x, const double *tab, int tanh_form
   return y;
 }
 
-// Four elements at once: the four erf evaluations share one (rarely taken)
-// branch into the exception table.  Same results as gelu1 element by element.
-__device__ __forceinline__ float4 gelu4(float4 v, const double *tab, int tanh_form) {
-  if (tanh_form)
-    return make_float4(gelu1(v.x, tab, 1), gelu1(v.y, tab, 1), gelu1(v.z, tab, 1), gelu1(v.w, tab, 1));
+// Four elements at once, the same results as gelu1 element by element.  The
+// four erf evaluations share one (rarely taken) branch into the exception
+// table.  NaN inputs need no select: x*SQRT_2_INV is the quieted x, its
+// magnitude clamps (erf = 1, ev = +-1), and (0.5f*x)*(1 + ev) multiplies the
+// quieted x, payload kept, by 2 or 0, which returns it.
+template <int TANH>
+__device__ __forceinline__ float4 gelu4(float4 v, const double *tab) {
+  if (TANH) return make_float4(gelu1<1>(v.x, tab), gelu1<1>(v.y, tab), gelu1<1>(v.z, tab), gelu1<1>(v.w, tab));
   const float x[4] = {v.x, v.y, v.z, v.w};
-  uint32_t ux[4], ax[4], r[4];
-  bool u[4];
+  float xs[4];
+  uint32_t r[4], d[4];
 #pragma unroll
   for (int k = 0; k < 4; k++) {
-    ux[k] = f_bits(x[k] * bits_f(0x3F3504F3u));  // SQRT_2_INV
-    ax[k] = ux[k] & 0x7FFFFFFFu;
-    r[k] = erffk::erf_abs_bits_fast(ax[k], tab, &u[k]);
+    xs[k] = x[k] * bits_f(0x3F3504F3u);  // SQRT_2_INV
+    const double R = erffk::erf_abs_R(__builtin_fabsf(xs[k]), tab);
+    r[k] = f_bits((float)R);
+    d[k] = erffk::undecided_distance(R);
   }
-  if (u[0] | u[1] | u[2] | u[3]) {
+  const uint32_t dmin = std::min(std::min(d[0], d[1]), std::min(d[2], d[3]));
+  if (dmin < 0x40u) {
 #pragma unroll
     for (int k = 0; k < 4; k++)
-      if (u[k]) r[k] = erffk::exception_lookup(ax[k], r[k]);
+      if (d[k] < 0x40u) r[k] = erffk::exception_lookup(f_bits(xs[k]) & 0x7FFFFFFFu, r[k]);
   }
   float y[4];
 #pragma unroll
   for (int k = 0; k < 4; k++) {
-    r[k] = ax[k] >= erffk::kOneBits ? 0x3F800000u : r[k];
-    const float ev = bits_f(r[k] | (ux[k] & 0x80000000u));
+    const float ev = bits_f(r[k] | (f_bits(xs[k]) & 0x80000000u));
     y[k] = (0.5f * x[k]) * (1.0f + ev);
-    // A NaN input gives the input quieted, payload kept (Shaders.lean:196-199).
-    if ((f_bits(x[k]) & 0x7FFFFFFFu) > 0x7F800000u) y[k] = bits_f(f_bits(x[k]) | 0x00400000u);
   }
   return make_float4(y[0], y[1], y[2], y[3]);
 }
 
-// Two float4 per thread per iteration, both loads issued before the math.
-__global__ void __launch_bounds__(256) gelu_erf_k(int64_t n, int tanh_form, const float *__restrict__ X,
+// Block b owns the float4s [b*chunk, (b+1)*chunk) (contiguous, so each block
+// streams whole DRAM pages); each thread takes kGeluU float4s 256 apart per
+// step.  The first step's loads are issued before the table is staged in LDS,
+// so they are in flight during the staging.  The last block also maps the
+// n % 4 scalar tail.
+constexpr int kGeluU = 4;
+
+template <int TANH>
+__global__ void __launch_bounds__(256) gelu_erf_k(int64_t n, int64_t chunk, const float *__restrict__ X,
                                                   float *__restrict__ Y) {
   __shared__ double tab[kPolyWords];
-  load_poly(tab);
   const int64_t n4 = n / 4;
-  const int64_t stride = (int64_t)gridDim.x * blockDim.x;
-  int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x;
-  for (; i + stride < n4; i += 2 * stride) {
-    const float4 v0 = ld4(X + 4 * i), v1 = ld4(X + 4 * (i + stride));
-    st4(Y + 4 * i, gelu4(v0, tab, tanh_form));
-    st4(Y + 4 * (i + stride), gelu4(v1, tab, tanh_form));
+  const int64_t b0 = blockIdx.x * chunk;
+  const int64_t e = b0 + chunk < n4 ? b0 + chunk : n4;
+  int64_t i = b0 + threadIdx.x;
+  float4 v[kGeluU];
+  bool loaded = i + (kGeluU - 1) * 256 < e;
+  if (loaded) {
+#pragma unroll
+    for (int u = 0; u < kGeluU; u++) v[u] = ld4_nt(X + 4 * (i + u * 256));
   }
-  if (i < n4) st4(Y + 4 * i, gelu4(ld4(X + 4 * i), tab, tanh_form));
-  for (int64_t i = 4 * n4 + blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x)
-    Y[i] = gelu1(X[i], tab, tanh_form);
+  load_poly(tab);
+  for (; i + (kGeluU - 1) * 256 < e; i += kGeluU * 256) {
+    if (!loaded) {
+#pragma unroll
+      for (int u = 0; u < kGeluU; u++) v[u] = ld4_nt(X + 4 * (i + u * 256));
+    }
+    loaded = false;
+#pragma unroll
+    for (int u = 0; u < kGeluU; u++) st4_nt(Y + 4 * (i + u * 256), gelu4<TANH>(v[u], tab));
+  }
+  for (; i < e; i += 256) st4_nt(Y + 4 * i, gelu4<TANH>(ld4_nt(X + 4 * i), tab));
+  if (blockIdx.x == gridDim.x - 1)
+    for (int64_t t = 4 * n4 + threadIdx.x; t < n; t += 256) Y[t] = gelu1<TANH>(X[t], tab);
 }
 
 __global__ void __launch_bounds__(256) erff_map_k(uint32_t base, uint32_t count, uint32_t *__restrict__ Y) {
@@ -865,15 +921,27 @@ ArrayP gelu_erf(const ArrayP &x0, bool tanh_form) {
   auto y = new_array(kF32, x->shape);
   const int64_t n = x->size();
   if (!n) return y;
+  if ((uintptr_t)x->data() % 16) {  // a view at an odd offset: the float4 path needs an aligned copy
+    auto c = new_array(kF32, x->shape);
+    copy_into(c, x);
+    x = c;
+  }
   const float *px = (const float *)x->data();
   float *py = (float *)y->data();
-  if (((uintptr_t)px | (uintptr_t)py) % 16) fail("ggml.gelu_erf: operands must be 16-byte aligned");
   const int tf = tanh_form ? 1 : 0;
   ArrayP kx = x;
-  const unsigned grid = grid_cap(n / 4 + 1, 256, 256 * 8);
+  // 8192 blocks (32 per CU) of at least 4 float4 steps each
+  static const int blocks = env_int("SHLO_GELU_BLOCKS", 8192);
+  const int64_t n4 = n / 4;
+  const int64_t per = kGeluU * 256;
+  const int64_t steps = std::max<int64_t>(1, (n4 + per - 1) / per);
+  const int64_t nb = std::max<int64_t>(1, std::min<int64_t>(blocks, steps));
+  const int64_t chunk = (steps + nb - 1) / nb * per;
+  const unsigned grid = (unsigned)std::max<int64_t>(1, (n4 + chunk - 1) / chunk);
   launch([=](hipStream_t s) {
     (void)kx;
-    gelu_erf_k<<<grid, 256, 0, s>>>(n, tf, px, py);
+    if (tf) gelu_erf_k<1><<<grid, 256, 0, s>>>(n, chunk, px, py);
+    else gelu_erf_k<0><<<grid, 256, 0, s>>>(n, chunk, px, py);
   });
   return y;
 }

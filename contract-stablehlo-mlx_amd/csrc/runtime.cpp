@@ -1,7 +1,9 @@
 // Device-array runtime: pool, stream, tracing and hipGraph replay.
 #include "runtime.h"
 
+#include <algorithm>
 #include <cstdarg>
+#include <cstdlib>
 #include <map>
 #include <mutex>
 
@@ -299,6 +301,26 @@ struct TraceScope {
 };
 }  // namespace
 
+// Traces of fewer launches than this replay their recorded launches straight
+// onto the stream; longer ones are captured into a hipGraph.  A graph launch
+// costs the stream a gap of several microseconds before its first kernel, more
+// than issuing a few dozen kernels (which queue back to back behind a busy
+// GPU); a graph saves host time on long traces.  SHLO_GRAPH_MIN_OPS sets the
+// initial value.
+static size_t &graph_min_ops_ref() {
+  static size_t n = [] {
+    const char *e = getenv("SHLO_GRAPH_MIN_OPS");
+    return e ? (size_t)std::max(1, atoi(e)) : (size_t)32;
+  }();
+  return n;
+}
+size_t graph_min_ops() { return graph_min_ops_ref(); }
+size_t set_graph_min_ops(size_t n) {
+  const size_t prev = graph_min_ops_ref();
+  graph_min_ops_ref() = std::max<size_t>(1, n);
+  return prev;
+}
+
 static CompiledFn::Variant &variant_for(CompiledFn &f, const std::vector<ArrayP> &in) {
   for (auto &v : f.variants) {
     if (v->sig.size() != in.size()) continue;
@@ -320,7 +342,7 @@ static CompiledFn::Variant &variant_for(CompiledFn &f, const std::vector<ArrayP>
     std::vector<ArrayP> outs = f.fn(ins);
     for (auto &o : outs) v->outs.push_back(o->contiguous() ? o : contiguous(o));
   }
-  if (!v->trace.ops.empty()) {
+  if (v->trace.ops.size() >= graph_min_ops()) {
     hipStream_t s = stream();
     SHLO_HIP(hipStreamBeginCapture(s, hipStreamCaptureModeThreadLocal));
     try {
@@ -350,6 +372,8 @@ std::vector<ArrayP> apply_fn(CompiledFn &f, const std::vector<ArrayP> &inputs) {
   }
   if (v.exec) {
     SHLO_HIP(hipGraphLaunch(v.exec, s));
+  } else {
+    for (auto &op : v.trace.ops) op(s);  // a short trace: its launches, re-issued
   }
   std::vector<ArrayP> res;
   for (auto &o : v.outs) {

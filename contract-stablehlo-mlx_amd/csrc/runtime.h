@@ -121,4 +121,9 @@ struct CompiledFn {
 
 std::vector<ArrayP> apply_fn(CompiledFn &f, const std::vector<ArrayP> &inputs);
 
+// Fewest recorded launches a compiled function captures into a hipGraph
+// (shorter traces re-issue their launches); the setter returns the old value.
+size_t graph_min_ops();
+size_t set_graph_min_ops(size_t n);
+
 }  // namespace shlo

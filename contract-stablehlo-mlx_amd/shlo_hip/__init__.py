@@ -417,6 +417,15 @@ def get_flavor():
     return _lib.shlo_get_flavor()
 
 
+def set_graph_min_ops(n):
+    """Compiled functions traced from now on capture a hipGraph when their
+    trace holds at least n launches (shorter ones re-issue the launches).
+    Returns the previous value."""
+    prev = ctypes.c_int()
+    _check(_lib.shlo_set_graph_min_ops(ctypes.c_int(n), ctypes.byref(prev)))
+    return prev.value
+
+
 def fill_random(shape, seed, dist, param, skip=0) -> Arr:
     s, r = _i64(shape)
     h = _out()

@@ -193,6 +193,16 @@ int shlo_call(shlo_fn *f, const shlo_arr *const *inputs, size_t nin, shlo_arr **
 int shlo_set_flavor(int flavor);
 int shlo_get_flavor(void);
 
+/* Compiled functions (shlo_compile, shlo_module_prepare with compile = 1)
+ * whose trace holds at least n recorded launches are captured into one
+ * hipGraph; shorter traces re-issue their recorded launches on the stream
+ * (same kernels, same buffers, same bits).  Takes effect for functions traced
+ * afterwards (a function is traced on its first call per input signature).
+ * Default 32 (or the environment's SHLO_GRAPH_MIN_OPS); n = 1 captures every
+ * trace.  *prev receives the old value when prev is not NULL.  Not in the
+ * reference (mlx compiles to its own graph). */
+int shlo_set_graph_min_ops(int n, int *prev);
+
 /* Measurement helpers (not in the reference): a device-side fill from the
  * splitmix32 stream of ref/ggml_ref.c:21-30 — dist 0: unif(a) with a =
  * param (ggml_ref.c:30), element i using draw i; dist 1: the Irwin-Hall

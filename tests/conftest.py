@@ -52,3 +52,13 @@ def ref_pinned(tmp_path_factory):
 def ref_stock(tmp_path_factory):
     """Every ggml_ref case written by the oracle, stock flavour."""
     return _write_refs(tmp_path_factory, "stock")
+
+
+@pytest.fixture(params=["graph", "replay"])
+def graph_mode(request):
+    """Compiled functions traced in the test either captured into a hipGraph
+    ("graph": every trace) or re-issuing their recorded launches ("replay")."""
+    import shlo_hip
+    prev = shlo_hip.set_graph_min_ops(1 if request.param == "graph" else 1 << 30)
+    yield request.param
+    shlo_hip.set_graph_min_ops(prev)

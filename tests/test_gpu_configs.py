@@ -4,7 +4,7 @@ bit against the oracle; each with its planted wrong lowering."""
 import numpy as np
 import pytest
 
-pytestmark = pytest.mark.gpu
+pytestmark = [pytest.mark.gpu, pytest.mark.usefixtures("graph_mode")]
 
 
 def dot_module(N, K, M, batch=0):
@@ -160,10 +160,41 @@ def test_gelu_config2b(oracle):
     assert not same_bits(f[:1 << 20], gs[:1 << 20])
 
 
+@pytest.mark.parametrize("n", [1, 3, 4, 5, 1027, 4096 + 3, 262147, 3 * 1024 * 1024 + 5])
+def test_gelu_lengths(oracle, n):
+    """Lengths with every n % 4 (the scalar tail), below one block's step and
+    spread over many blocks' chunks."""
+    x, _ = oracle.fill_normal(13, 3.0, n)
+    got = run(custom_call_module("ggml.gelu_erf", "", (n,)), [x])[0]
+    assert same_bits(got, oracle.gelu_erf(x))
+
+
+@pytest.mark.parametrize("off", [1, 2, 3, 4])
+def test_gelu_on_offset_view(oracle, off):
+    """GELU of a slice starting `off` elements in (a view that is not 16-byte
+    aligned unless off % 4 == 0)."""
+    n = 70000
+    x, _ = oracle.fill_normal(14, 3.0, n + off)
+    t_in, t_out = f"tensor<{n + off}xf32>", f"tensor<{n}xf32>"
+    text = (f"module {{\n  func.func public @main(%a0: {t_in}) -> ({t_out}) {{\n"
+            f'    %0 = "stablehlo.slice"(%a0) {{start_indices = array<i64: {off}>, limit_indices = '
+            f"array<i64: {n + off}>, strides = array<i64: 1>}} : ({t_in}) -> {t_out}\n"
+            f'    %1 = "stablehlo.custom_call"(%0) {{call_target_name = "ggml.gelu_erf", backend_config = ""}}'
+            f" : ({t_out}) -> {t_out}\n    func.return %1 : {t_out}\n  }}\n}}\n")
+    for compile in (True, False):
+        got = run(text, [x], compile=compile)[0]
+        assert same_bits(got, oracle.gelu_erf(x[off:]))
+
+
 def test_gelu_special_values(oracle):
     specials = np.array([0.0, -0.0, np.inf, -np.inf, 1e-45, -1e-45, 1e-38, 3.0, -3.0, 5.5, -5.5, 87.0, -87.0,
                          3.4028235e38, -3.4028235e38], np.float32)
-    nan = np.array([0x7FC00000, 0x7F800001, 0xFFC01234, 0x7FBFFFFF], np.uint32).view(np.float32)
+    nan = np.array([0x7FC00000, 0x7F800001, 0xFFC01234, 0x7FBFFFFF, 0xFF800001, 0xFFFFFFFF], np.uint32)
+    # random payloads, both signs, quiet and signalling
+    rng = np.random.default_rng(5)
+    payload = rng.integers(1, 1 << 23, 250, dtype=np.uint32)
+    sign = rng.integers(0, 2, 250, dtype=np.uint32) << 31
+    nan = np.concatenate([nan, sign | 0x7F800000 | payload]).view(np.float32)
     x = np.concatenate([specials, nan, np.zeros(1, np.float32)])
     want = oracle.gelu_erf(x)
     got = run(custom_call_module("ggml.gelu_erf", "", x.shape), [x])[0]

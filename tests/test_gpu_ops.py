@@ -4,7 +4,7 @@ the reference's Tests/OpTests.lean:180-222)."""
 import numpy as np
 import pytest
 
-pytestmark = pytest.mark.gpu
+pytestmark = [pytest.mark.gpu, pytest.mark.usefixtures("graph_mode")]
 
 
 def _tally_case(ref, name, pinned=False):

@@ -4,7 +4,7 @@ paths (the shim contracts of c/smlx_shim.c:299-386)."""
 import numpy as np
 import pytest
 
-pytestmark = pytest.mark.gpu
+pytestmark = [pytest.mark.gpu, pytest.mark.usefixtures("graph_mode")]
 
 
 def same_bits(a, b):
