@@ -139,11 +139,13 @@ typedef int (*shlo_traced_fn)(void *payload, const shlo_arr *const *inputs, size
                               size_t out_cap, size_t *nout);
 
 /* smlx_compile (c/smlx_shim.c:359-374): wrap `fn`.  With enable != 0 the first
- * apply for each input signature traces `fn` (its ops are recorded, not run),
- * captures the recorded launches into a hipGraph and instantiates it; every
- * apply then copies the inputs into the graph's input buffers (skipped when
- * the same array is passed again), launches the graph and returns fresh
- * output arrays.  With enable == 0 every apply calls `fn` eagerly.
+ * apply for each input signature traces `fn` (its ops are recorded, not run)
+ * and captures the recorded launches into a hipGraph (traces shorter than
+ * shlo_set_graph_min_ops' threshold keep the recorded launches instead); every
+ * apply then copies the inputs into the trace's input buffers (skipped when
+ * the same array is passed again), launches the graph (or re-issues the
+ * launches) and returns fresh output arrays.  With enable == 0 every apply
+ * calls `fn` eagerly.
  * payload_free (may be NULL) is called on payload when the fn is freed. */
 int shlo_compile(shlo_traced_fn fn, void *payload, void (*payload_free)(void *), int enable, shlo_fn **out);
 void shlo_fn_free(shlo_fn *f);
