@@ -295,7 +295,7 @@ def cpu_baseline(reps=2):
         t_sm, t_ge = t_sm + (t1 - t0), t_ge + (t2 - t1)
     nbytes = reps * (8 * rows * cols + 8 * n)
     return {"value": round(nbytes / (t_sm + t_ge) / 1e9, 3), "unit": "GB/s", "cores": cores, "kind": "port",
-            "sample": f"the full workload {reps}x: oracle ggml.soft_max [4096,1024] ({t_sm:.2f} s) + oracle "
+            "sample": f"the full workload {reps}x: oracle ggml.soft_max [4096,1024] ({t_sm:.3f} s) + oracle "
                       f"erf-GELU (libquadmath erfq per element) over 64 Mi ({t_ge:.2f} s)"}
 
 

@@ -195,7 +195,7 @@ int shlo_eval(const shlo_arr *const *xs, size_t n) {
 
 // ---- kernels ---------------------------------------------------------------------
 
-static const char *kKernels[] = {"mul_mat", "soft_max", "norm", "silu", "gelu_erf", "erff_map",
+static const char *kKernels[] = {"mul_mat", "soft_max", "norm", "silu", "gelu_erf", "erff_map", "expf_map",
                                  "divide", "sqrt", "f64_ew", "f64_of_f32", "f32_of_f64"};
 
 int shlo_kernel_new(const char *name, const char *const *inputs, size_t nin, const char *const *outputs, size_t nout,
@@ -258,6 +258,10 @@ int shlo_kernel_apply(const shlo_kernel *k, const shlo_arr *const *inputs, size_
       want(2);
       auto p = params_of(in[1]);
       y = erff_map(p[0], p[1]);
+    } else if (n == "expf_map") {  // [p = base, count]: the row tails' correctly rounded expf (no reference kernel)
+      want(1);
+      auto p = params_of(in[0]);
+      y = expf_map(p[0], p[1]);
     } else if (n == "divide") {  // [a, b, p = count]
       want(3);
       y = divide_exact(in[0], in[1]);
@@ -350,6 +354,16 @@ int shlo_libm_erff_range(uint32_t base, uint32_t count, uint32_t *out) {
     if (count) need(out, "out");
     for (uint32_t i = 0; i < count; i++) {
       const float y = shlo::erff_host(__builtin_bit_cast(float, base + i));
+      out[i] = __builtin_bit_cast(uint32_t, y);
+    }
+  });
+}
+
+int shlo_expf_range(uint32_t base, uint32_t count, uint32_t *out) {
+  return guard("expf_range", [&] {
+    if (count) need(out, "out");
+    for (uint32_t i = 0; i < count; i++) {
+      const float y = shlo::expf_host(__builtin_bit_cast(float, base + i));
       out[i] = __builtin_bit_cast(uint32_t, y);
     }
   });

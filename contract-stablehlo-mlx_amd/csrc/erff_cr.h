@@ -48,20 +48,19 @@ __host__ __device__ inline uint32_t exception_lookup(uint32_t ax, uint32_t fallb
 constexpr float kClampA = 3.984375f;
 constexpr uint32_t kClampBits = 0x407F0000u;
 
-// R ~ erf(min(a, kClampA)) in binary64 for a = |x| >= 0 or a quiet NaN (which
-// clamps too: v_min_f32 and fminf return the number), branch-free:
-// R = a * Q_i(u) with i = floor(64 a) and u = 64 a - i (exact in binary32),
-// Q_i row i of `tab`.
-__host__ __device__ inline double erf_abs_R(float a, const double *tab) {
-  const float ac = __builtin_fminf(a, kClampA);
-  const float a64 = ac * 64.0f;  // exact scaling, <= 255
-  const unsigned i = (unsigned)(int)a64 & (unsigned)(kTab - 1);
+// R ~ erf(a64 / 64) in binary64 for a64 in [0, 255] (a quiet NaN is clamped
+// there by the callers' v_min_f32 / fminf, which return the number),
+// branch-free: i = floor(a64), u = a64 - i, R = a64 * (Q_i(u) / 64) with row i
+// of `tab` holding Q_i / 64.  u is exact (the fraction of a binary64 copy of a
+// binary32).
+__host__ __device__ inline double erf_R64(float a64, const double *tab) {
+  const double ad = (double)a64;
 #if defined(__HIP_DEVICE_COMPILE__)
-  const float uf = __builtin_amdgcn_fractf(a64);  // a64 - floor(a64), exact for a64 >= 0
+  const double u = __builtin_amdgcn_fract(ad);  // ad - floor(ad), exact for ad >= 0
 #else
-  const float uf = a64 - (float)(int)a64;  // exact (Sterbenz for a64 >= 1)
+  const double u = ad - __builtin_floor(ad);
 #endif
-  const double u = (double)uf;
+  const unsigned i = (unsigned)(int)a64 & (unsigned)(kTab - 1);
   const double *p = tab + 6 * i;
   double q = p[5];
   q = __builtin_fma(q, u, p[4]);
@@ -69,7 +68,12 @@ __host__ __device__ inline double erf_abs_R(float a, const double *tab) {
   q = __builtin_fma(q, u, p[2]);
   q = __builtin_fma(q, u, p[1]);
   q = __builtin_fma(q, u, p[0]);
-  return (double)ac * q;
+  return ad * q;
+}
+
+// R ~ erf(min(a, kClampA)) for a = |x| >= 0 or a quiet NaN.
+__host__ __device__ inline double erf_abs_R(float a, const double *tab) {
+  return erf_R64(__builtin_fminf(a, kClampA) * 64.0f, tab);  // exact scaling
 }
 
 // The binary32 rounding of R is decided by R's low 29 fraction bits: it is

@@ -8,6 +8,7 @@
 #include <type_traits>
 
 #include "erff_cr.h"
+#include "expf_cr.h"
 #include "ggml_expf.h"
 #include "ops.h"
 
@@ -26,6 +27,24 @@ __device__ __forceinline__ void wave_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 __device__ __forceinline__ void st4(float *p, float4 v) { *reinterpret_cast<float4 *>(p) = v; }
+
+// Streaming loads and stores for operands touched once: they bypass cache
+// allocation (the `nt` bit).
+__device__ __forceinline__ float4 ld4_nt(const float *p) {
+  float4 v;
+  v.x = __builtin_nontemporal_load(p);
+  v.y = __builtin_nontemporal_load(p + 1);
+  v.z = __builtin_nontemporal_load(p + 2);
+  v.w = __builtin_nontemporal_load(p + 3);
+  return v;
+}
+__device__ __forceinline__ void st4_nt(float *p, float4 v) {
+  __builtin_nontemporal_store(v.x, p);
+  __builtin_nontemporal_store(v.y, p + 1);
+  __builtin_nontemporal_store(v.z, p + 2);
+  __builtin_nontemporal_store(v.w, p + 3);
+}
+
 
 // ---- dot_general in ggml_vec_dot_f32 order --------------------------------------
 
@@ -306,6 +325,11 @@ __device__ __forceinline__ double chain_sum_f64(const T *p, int n) {
   return s;
 }
 
+// Doubles per row of parts in soft_max_rows_k: a multiple of 2 (16-byte rows
+// for the chain's double2 reads) with 2 spare, so the RB rows start in
+// different banks.
+__host__ __device__ inline int softmax_rows_part_stride(int G) { return (G + 1) / 2 * 2 + 2; }
+
 // ggml soft_max.  Lane l of a row's wave owns the four-element groups
 // g = l + 64j, loaded as float4 (coalesced).  The row maximum is a wave
 // reduction (exact: max is order-free on non-NaN data, and a +0/-0 tie
@@ -314,36 +338,45 @@ __device__ __forceinline__ double chain_sum_f64(const T *p, int n) {
 // part is added to a binary64 sum in group order (ggml_vec_soft_max_f32,
 // Shaders.lean:111-120); inv = (float)(1.0/sum), then y = e*inv.
 //
-// A block of 4*RPW rows: wave w computes rows w, w+4, ... as above (coalesced
-// float4 loads, wave max, ggml_v_expf values kept in registers) and writes
-// each group's part to LDS, one padded row per row.  Then lane r of wave 0
-// runs row r's binary64 sum over the parts in group order, so one v_add_f64
-// advances 4*RPW rows and the parts come from LDS without bank conflicts;
-// the other waves wait at the barrier.  Finally every wave scales and stores.
+// A block of 4*RPW rows: wave w loads rows w, w+4, ... (all loads first,
+// nontemporal: each byte is read once), then per row takes the wave max, keeps
+// the ggml_v_expf values in registers and writes each group's part to LDS as
+// binary64 (the conversion runs on every lane, off the serial path), one padded
+// row per row.  Then lane r of wave 0 runs row r's binary64 sum over the parts
+// in group order, so one v_add_f64 advances 4*RPW rows; the other waves wait
+// at the barrier.  Finally every wave scales and stores.
 template <int J, int RPW>
 __global__ void __launch_bounds__(256) soft_max_rows_k(int64_t rows, int cols, float sc, int float_sum,
                                                        const float *__restrict__ X, float *__restrict__ Y) {
-  extern __shared__ float lds[];
+  extern __shared__ double lds_d[];
   constexpr int RB = 4 * RPW;
   const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
   const int G = cols / 4;
-  const int PS = (G + 3) / 4 * 4 + 4;
-  float *parts = lds;
-  float *invs = lds + RB * PS;
+  const int PS = softmax_rows_part_stride(G);
+  double *parts = lds_d;
+  float *invs = reinterpret_cast<float *>(lds_d + RB * PS);
   const int64_t row0 = blockIdx.x * (int64_t)RB;
   float4 e[RPW][J];
 #pragma unroll
   for (int rr = 0; rr < RPW; rr++) {
-    const int lr = wave + 4 * rr;
-    const int64_t row = row0 + lr;
+    const int64_t row = row0 + wave + 4 * rr;
     if (row >= rows) continue;
     const float *x = X + row * cols;
+#pragma unroll
+    for (int j = 0; j < J; j++) {
+      const int g = lane + kWave * j;
+      if (g < G) e[rr][j] = ld4_nt(x + 4 * g);
+    }
+  }
+#pragma unroll
+  for (int rr = 0; rr < RPW; rr++) {
+    const int lr = wave + 4 * rr;
+    if (row0 + lr >= rows) continue;
     float mx = -__builtin_inff();
 #pragma unroll
     for (int j = 0; j < J; j++) {
       const int g = lane + kWave * j;
       if (g < G) {
-        e[rr][j] = ld4(x + 4 * g);
         const float w0 = e[rr][j].x * sc, w1 = e[rr][j].y * sc, w2 = e[rr][j].z * sc, w3 = e[rr][j].w * sc;
         mx = mx > w0 ? mx : w0;
         mx = mx > w1 ? mx : w1;
@@ -364,17 +397,17 @@ __global__ void __launch_bounds__(256) soft_max_rows_k(int64_t rows, int cols, f
         e[rr][j].y = ggml_v_expf(e[rr][j].y * sc - mx);
         e[rr][j].z = ggml_v_expf(e[rr][j].z * sc - mx);
         e[rr][j].w = ggml_v_expf(e[rr][j].w * sc - mx);
-        parts[lr * PS + g] = (e[rr][j].x + e[rr][j].y) + (e[rr][j].z + e[rr][j].w);
+        parts[lr * PS + g] = (double)((e[rr][j].x + e[rr][j].y) + (e[rr][j].z + e[rr][j].w));
       }
     }
   }
   __syncthreads();
   if (wave == 0 && lane < RB && row0 + lane < rows) {
-    const float *pr = parts + lane * PS;
+    const double *pr = parts + lane * PS;
     float inv;
     if (float_sum) {  // planted: the denominator summed in binary32 (Shaders.lean:120-122)
       float fs = 0.0f;
-      for (int g = 0; g < G; g++) fs = fs + pr[g];
+      for (int g = 0; g < G; g++) fs = fs + (float)pr[g];
       inv = 1.0f / fs;
     } else {
       inv = (float)(1.0 / chain_sum_f64(pr, G));
@@ -392,9 +425,92 @@ __global__ void __launch_bounds__(256) soft_max_rows_k(int64_t rows, int cols, f
 #pragma unroll
     for (int j = 0; j < J; j++) {
       const int g = lane + kWave * j;
-      if (g < G) st4(y + 4 * g, make_float4(e[rr][j].x * inv, e[rr][j].y * inv, e[rr][j].z * inv, e[rr][j].w * inv));
+      if (g < G) st4_nt(y + 4 * g, make_float4(e[rr][j].x * inv, e[rr][j].y * inv, e[rr][j].z * inv, e[rr][j].w * inv));
     }
   }
+}
+
+// Rows whose length is not a multiple of 4 (the pinned flavour only): ggml
+// runs the four-lane body over the first 4*G elements and sends the last
+// cols % 4 through the scalar expf, the correctly rounded one here, adding
+// each tail value to the binary64 sum after the group parts
+// (ggml_vec_soft_max_f32).  Rows are not 16-byte aligned, so elements are read
+// one by one; wave w of a block owns row 4*blockIdx.x + w and its lane 0 runs
+// the row's sum.
+template <int J>
+__global__ void __launch_bounds__(256) soft_max_tail_k(int64_t rows, int cols, float sc, int float_sum,
+                                                       const float *__restrict__ X, float *__restrict__ Y) {
+  extern __shared__ double lds_t[];
+  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  const int G = cols / 4, T = cols % 4;
+  double *parts = lds_t + wave * softmax_rows_part_stride(G + T);
+  const int64_t row = blockIdx.x * 4LL + wave;
+  if (row >= rows) return;  // the whole wave: no block barrier follows
+  const float *x = X + row * cols;
+  float *y = Y + row * cols;
+  float4 e[J];
+  float et = 0.0f;
+  float mx = -__builtin_inff();
+#pragma unroll
+  for (int j = 0; j < J; j++) {
+    const int g = lane + kWave * j;
+    if (g < G) {
+      e[j] = make_float4(x[4 * g], x[4 * g + 1], x[4 * g + 2], x[4 * g + 3]);
+      const float w0 = e[j].x * sc, w1 = e[j].y * sc, w2 = e[j].z * sc, w3 = e[j].w * sc;
+      mx = mx > w0 ? mx : w0;
+      mx = mx > w1 ? mx : w1;
+      mx = mx > w2 ? mx : w2;
+      mx = mx > w3 ? mx : w3;
+    }
+  }
+  if (lane < T) {
+    et = x[4 * G + lane];
+    const float w = et * sc;
+    mx = mx > w ? mx : w;
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    const float other = __shfl_xor(mx, o, kWave);
+    mx = mx > other ? mx : other;
+  }
+#pragma unroll
+  for (int j = 0; j < J; j++) {
+    const int g = lane + kWave * j;
+    if (g < G) {
+      e[j].x = ggml_v_expf(e[j].x * sc - mx);
+      e[j].y = ggml_v_expf(e[j].y * sc - mx);
+      e[j].z = ggml_v_expf(e[j].z * sc - mx);
+      e[j].w = ggml_v_expf(e[j].w * sc - mx);
+      parts[g] = (double)((e[j].x + e[j].y) + (e[j].z + e[j].w));
+    }
+  }
+  if (lane < T) {
+    et = expfk::expf_cr(et * sc - mx);
+    parts[G + lane] = (double)et;
+  }
+  wave_sync();
+  float inv = 0.0f;
+  if (lane == 0) {
+    if (float_sum) {  // planted: the denominator summed in binary32 (Shaders.lean:120-122)
+      float fs = 0.0f;
+      for (int g = 0; g < G + T; g++) fs = fs + (float)parts[g];
+      inv = 1.0f / fs;
+    } else {
+      inv = (float)(1.0 / chain_sum_f64(parts, G + T));
+    }
+  }
+  inv = __shfl(inv, 0, kWave);
+#pragma unroll
+  for (int j = 0; j < J; j++) {
+    const int g = lane + kWave * j;
+    if (g < G) {
+      y[4 * g] = e[j].x * inv;
+      y[4 * g + 1] = e[j].y * inv;
+      y[4 * g + 2] = e[j].z * inv;
+      y[4 * g + 3] = e[j].w * inv;
+    }
+  }
+  if (lane < T) y[4 * G + lane] = et * inv;
 }
 
 // Doubles per row of parts in soft_max_pipe_k: even, so every row starts
@@ -585,11 +701,17 @@ __global__ void __launch_bounds__(256) norm_k(int64_t rows, int cols, float eps,
 
 // x / (1 + ggml_v_expf(0 - x)) on the four-lane body (Shaders.lean:172-179);
 // rows must be multiples of 4 (tails are refused by the lowering).
-__global__ void __launch_bounds__(256) silu_k(int64_t n, int gpu_ops, const float *__restrict__ X,
+// With rows of `cols` not a multiple of 4 (pinned flavour only), each row's
+// last cols % 4 elements take x / (1 + expf(-x)) with the correctly rounded
+// expf (ggml_vec_silu_f32's scalar loop).
+template <int TAIL>
+__global__ void __launch_bounds__(256) silu_k(int64_t n, int64_t cols, int gpu_ops, const float *__restrict__ X,
                                               float *__restrict__ Y) {
+  const int64_t body = cols & ~(int64_t)3;
   for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n; i += (int64_t)gridDim.x * blockDim.x) {
     const float x = X[i];
     if (gpu_ops) Y[i] = x * __builtin_amdgcn_rcpf(1.0f + __expf(-x));  // planted: GPU exp and /
+    else if (TAIL && i % cols >= body) Y[i] = x / (1.0f + expfk::expf_cr(-x));
     else Y[i] = x / (1.0f + ggml_v_expf(0.0f - x));
   }
 }
@@ -606,23 +728,6 @@ __device__ __forceinline__ void load_poly(double *tab) {
   __syncthreads();
 }
 
-// Streaming loads and stores: each byte of a unary map's operands is touched
-// once, so they bypass cache allocation (the `nt` bit).
-__device__ __forceinline__ float4 ld4_nt(const float *p) {
-  float4 v;
-  v.x = __builtin_nontemporal_load(p);
-  v.y = __builtin_nontemporal_load(p + 1);
-  v.z = __builtin_nontemporal_load(p + 2);
-  v.w = __builtin_nontemporal_load(p + 3);
-  return v;
-}
-__device__ __forceinline__ void st4_nt(float *p, float4 v) {
-  __builtin_nontemporal_store(v.x, p);
-  __builtin_nontemporal_store(v.y, p + 1);
-  __builtin_nontemporal_store(v.z, p + 2);
-  __builtin_nontemporal_store(v.w, p + 3);
-}
-
 template <int TANH>
 __device__ __forceinline__ float gelu1(float x, const double *tab) {
   float ev;
@@ -636,21 +741,25 @@ __device__ __forceinline__ float gelu1(float x, const double *tab) {
   return y;
 }
 
-// Four elements at once, the same results as gelu1 element by element.  The
-// four erf evaluations share one (rarely taken) branch into the exception
-// table.  NaN inputs need no select: x*SQRT_2_INV is the quieted x, its
-// magnitude clamps (erf = 1, ev = +-1), and (0.5f*x)*(1 + ev) multiplies the
-// quieted x, payload kept, by 2 or 0, which returns it.
+// Four elements at once, the same results as gelu1 element by element.
+//
+// 64 |x*SQRT_2_INV| is taken as one product |x| * (64*SQRT_2_INV) (the
+// scaling is exact), clamped to 255: the same value wherever x*SQRT_2_INV is
+// a normal binary32, and where it is subnormal (|x| < 1.7e-38) erf of it is
+// below 2^-125, so 1 + ev rounds to 1 either way.  The four erf evaluations
+// share one (rarely taken) branch into the exception table, keyed by
+// |x*SQRT_2_INV|.  NaN inputs need no select: the clamp maps them to erf = 1,
+// ev = +-1, and (0.5f*x)*(1 + ev) multiplies the quieted x, payload kept, by
+// 2 or 0, which returns it.
 template <int TANH>
 __device__ __forceinline__ float4 gelu4(float4 v, const double *tab) {
   if (TANH) return make_float4(gelu1<1>(v.x, tab), gelu1<1>(v.y, tab), gelu1<1>(v.z, tab), gelu1<1>(v.w, tab));
   const float x[4] = {v.x, v.y, v.z, v.w};
-  float xs[4];
   uint32_t r[4], d[4];
 #pragma unroll
   for (int k = 0; k < 4; k++) {
-    xs[k] = x[k] * bits_f(0x3F3504F3u);  // SQRT_2_INV
-    const double R = erffk::erf_abs_R(__builtin_fabsf(xs[k]), tab);
+    const float a64 = __builtin_fminf(__builtin_fabsf(x[k]) * bits_f(0x423504F3u), 255.0f);  // 64*SQRT_2_INV
+    const double R = erffk::erf_R64(a64, tab);
     r[k] = f_bits((float)R);
     d[k] = erffk::undecided_distance(R);
   }
@@ -658,12 +767,12 @@ __device__ __forceinline__ float4 gelu4(float4 v, const double *tab) {
   if (dmin < 0x40u) {
 #pragma unroll
     for (int k = 0; k < 4; k++)
-      if (d[k] < 0x40u) r[k] = erffk::exception_lookup(f_bits(xs[k]) & 0x7FFFFFFFu, r[k]);
+      if (d[k] < 0x40u) r[k] = erffk::exception_lookup(f_bits(x[k] * bits_f(0x3F3504F3u)) & 0x7FFFFFFFu, r[k]);
   }
   float y[4];
 #pragma unroll
   for (int k = 0; k < 4; k++) {
-    const float ev = bits_f(r[k] | (f_bits(xs[k]) & 0x80000000u));
+    const float ev = bits_f(r[k] | (f_bits(x[k]) & 0x80000000u));
     y[k] = (0.5f * x[k]) * (1.0f + ev);
   }
   return make_float4(y[0], y[1], y[2], y[3]);
@@ -710,6 +819,11 @@ __global__ void __launch_bounds__(256) erff_map_k(uint32_t base, uint32_t count,
   load_poly(tab);
   for (uint32_t t = blockIdx.x * blockDim.x + threadIdx.x; t < count; t += gridDim.x * blockDim.x)
     Y[t] = f_bits(erffk::erff_cr(bits_f(base + t), tab));
+}
+
+__global__ void __launch_bounds__(256) expf_map_k(uint32_t base, uint32_t count, uint32_t *__restrict__ Y) {
+  for (uint32_t t = blockIdx.x * blockDim.x + threadIdx.x; t < count; t += gridDim.x * blockDim.x)
+    Y[t] = f_bits(expfk::expf_cr(bits_f(base + t)));
 }
 
 unsigned grid_cap(int64_t n, int block, int64_t cap) {
@@ -798,18 +912,51 @@ ArrayP mul_mat(const ArrayP &w0, const ArrayP &x0, int64_t K, int64_t M, int64_t
   return dot_ggml(DotOperand{x, N * K, K, 1}, DotOperand{w, wbs, K, 1}, B, N, M, K, tail);
 }
 
+// A row tail (cols % 4 elements) goes through ggml-cpu's scalar expf: the
+// pinned flavour's is correctly rounded and carried; the stock flavour's is
+// Apple libsystem_m's, closed code, and refused as the reference refuses it
+// (Lower.lean:485-486).
+void require_tail_expf(const char *op, int64_t cols) {
+  if (cols % 4 && default_dot_tail() != kTailPinned)
+    fail(strf("%s: a row of %lld has a %lld-element tail that ggml-cpu sends through the platform expf, which is "
+              "not carried (the pinned flavour carries it with the correctly rounded expf)",
+              op, (long long)cols, (long long)(cols % 4)));
+}
+
 ArrayP soft_max(const ArrayP &x0, int64_t rows, int64_t cols, uint32_t scale_bits, bool float_sum) {
   if (x0->dtype != kF32) fail("ggml.soft_max: f32 only");
   if (rows * cols != x0->size()) fail("ggml.soft_max: rows*cols is not the element count");
-  if (cols % 4)
-    fail(strf("ggml.soft_max: a row of %lld has a %lld-element tail that ggml-cpu sends through the platform "
-              "expf, which is not carried",
-              (long long)cols, (long long)(cols % 4)));
+  require_tail_expf("ggml.soft_max", cols);
   if (cols > 4 * kWave * 16) fail("ggml.soft_max: rows above 4096 columns are not carried");
   ArrayP x = contiguous(x0);
   auto y = new_array(kF32, x->shape);
   if (rows == 0 || cols == 0) return y;
   const float sc = bits_f(scale_bits);
+  if (cols % 4) {
+    const int G = (int)(cols / 4), T = (int)(cols % 4);
+    const int Jt = std::max(1, (G + kWave - 1) / kWave);
+    const int lds = 4 * softmax_rows_part_stride(G + T) * (int)sizeof(double);
+    const int64_t nblk = (rows + 3) / 4;
+    if (nblk > 0x7FFFFFFF) fail("ggml.soft_max: too many rows");
+    const unsigned grid = (unsigned)nblk;
+    const float *px = (const float *)x->data();
+    float *py = (float *)y->data();
+    const int c = (int)cols;
+    const int fs = float_sum ? 1 : 0;
+    ArrayP kx = x;
+    launch([=](hipStream_t s) {
+      (void)kx;
+#define SMT_CASE(n) \
+  case n: soft_max_tail_k<n><<<grid, 256, lds, s>>>(rows, c, sc, fs, px, py); break;
+      switch (Jt) {
+        SMT_CASE(1) SMT_CASE(2) SMT_CASE(3) SMT_CASE(4) SMT_CASE(5) SMT_CASE(6) SMT_CASE(7) SMT_CASE(8)
+        SMT_CASE(9) SMT_CASE(10) SMT_CASE(11) SMT_CASE(12) SMT_CASE(13) SMT_CASE(14) SMT_CASE(15) SMT_CASE(16)
+        default: break;
+      }
+#undef SMT_CASE
+    });
+    return y;
+  }
   const int J = (int)((cols / 4 + kWave - 1) / kWave);
   const int RPW = softmax_rows_per_wave(J);
   const float *px = (const float *)x->data();
@@ -843,8 +990,8 @@ ArrayP soft_max(const ArrayP &x0, int64_t rows, int64_t cols, uint32_t scale_bit
     });
     return y;
   }
-  const int PS = (int)((cols / 4 + 3) / 4 * 4 + 4);
-  const int lds = (4 * RPW * PS + 4 * RPW) * (int)sizeof(float);
+  const int PS = softmax_rows_part_stride((int)(cols / 4));
+  const int lds = 4 * RPW * PS * (int)sizeof(double) + 4 * RPW * (int)sizeof(float);
   const int64_t nblk = (rows + 4 * RPW - 1) / (4 * RPW);
   if (nblk > 0x7FFFFFFF) fail("ggml.soft_max: too many rows");
   const unsigned grid = (unsigned)nblk;
@@ -896,10 +1043,8 @@ ArrayP norm(const ArrayP &x0, int64_t rows, int64_t cols, uint32_t eps_bits, boo
 
 ArrayP silu(const ArrayP &x0, int64_t rows, int64_t cols, bool gpu_ops) {
   if (x0->dtype != kF32) fail("ggml.silu: f32 only");
-  if (cols % 4)
-    fail(strf("ggml.silu: a row of %lld has a %lld-element tail that ggml-cpu sends through the platform expf, "
-              "which is not carried",
-              (long long)cols, (long long)(cols % 4)));
+  require_tail_expf("ggml.silu", cols);
+  if (cols <= 0 && x0->size() > 0) fail("ggml.silu: rows of zero columns");
   ArrayP x = contiguous(x0);
   auto y = new_array(kF32, x->shape);
   const int64_t n = x->size();
@@ -908,9 +1053,11 @@ ArrayP silu(const ArrayP &x0, int64_t rows, int64_t cols, bool gpu_ops) {
   float *py = (float *)y->data();
   const int go = gpu_ops ? 1 : 0;
   ArrayP kx = x;
+  const int64_t c = cols;
   launch([=](hipStream_t s) {
     (void)kx;
-    silu_k<<<grid_cap(n, 256, 1 << 16), 256, 0, s>>>(n, go, px, py);
+    if (c % 4) silu_k<1><<<grid_cap(n, 256, 1 << 16), 256, 0, s>>>(n, c, go, px, py);
+    else silu_k<0><<<grid_cap(n, 256, 1 << 16), 256, 0, s>>>(n, c, go, px, py);
   });
   return y;
 }
@@ -963,6 +1110,16 @@ ArrayP sqrt_exact(const ArrayP &a) {
   if (a->dtype != kF32) fail("sqrt: f32 only");
   return unary(kSqrt, a);  // correctly rounded sqrtf (the default HIP lowering)
 }
+
+ArrayP expf_map(uint32_t base, uint32_t count) {
+  auto y = new_array(kU32, Shape{(int64_t)count});
+  if (!count) return y;
+  uint32_t *py = (uint32_t *)y->data();
+  launch([=](hipStream_t s) { expf_map_k<<<grid_cap(count, 256, 256 * 16), 256, 0, s>>>(base, count, py); });
+  return y;
+}
+
+float expf_host(float x) { return expfk::expf_cr(x); }
 
 float erff_host(float x) { return erffk::erff_cr(x, &erffk::kPoly[0][0]); }
 

@@ -498,18 +498,14 @@ struct Lowerer {
     auto rc = rows_cols(out);
     const int64_t rows = rc.first, cols = rc.second;
     if (name == "ggml.norm") return {reshape(norm(args.at(0), rows, cols, f32_attr(attrs, "eps"), f.norm_gpu_ops), out.dims)};
+    // A row tail (cols % 4) is refused unless the pinned flavour's correctly
+    // rounded expf carries it (Lower.lean:485-486 refuses it always).
     if (name == "ggml.soft_max") {
-      if (cols % 4 != 0)
-        fail(strf("ggml.soft_max: a row of %lld has a %lld-element tail that ggml-cpu sends through the platform "
-                  "expf, which is not carried",
-                  (long long)cols, (long long)(cols % 4)));
+      require_tail_expf("ggml.soft_max", cols);
       return {reshape(soft_max(args.at(0), rows, cols, f32_attr(attrs, "scale"), f.soft_max_float_sum), out.dims)};
     }
     if (name == "ggml.silu") {
-      if (cols % 4 != 0)
-        fail(strf("ggml.silu: a row of %lld has a %lld-element tail that ggml-cpu sends through the platform expf, "
-                  "which is not carried",
-                  (long long)cols, (long long)(cols % 4)));
+      require_tail_expf("ggml.silu", cols);
       return {reshape(silu(args.at(0), rows, cols, f.silu_gpu_ops), out.dims)};
     }
     if (name == "ggml.gelu_erf") return {reshape(gelu_erf(args.at(0), f.gelu_tanh), out.dims)};

@@ -83,13 +83,13 @@ ArrayP dot_ggml(const DotOperand &lhs, const DotOperand &rhs, int64_t B, int64_t
 ArrayP mul_mat(const ArrayP &w, const ArrayP &x, int64_t K, int64_t M, int64_t R, int64_t N,
                int64_t wBatchStride, int tail);
 
-// ggml soft_max over `rows` rows of `cols` (Shaders.lean:100-123).  cols must
-// be a multiple of 4 unless tails are enabled (the scalar expf is then the
-// correctly rounded one).
+// ggml soft_max over `rows` rows of `cols` (Shaders.lean:100-123).  A row
+// tail (cols % 4 elements) is carried in the pinned flavour only, through the
+// correctly rounded expf.
 ArrayP soft_max(const ArrayP &x, int64_t rows, int64_t cols, uint32_t scale_bits, bool float_sum);
 // ggml norm (Shaders.lean:130-166).
 ArrayP norm(const ArrayP &x, int64_t rows, int64_t cols, uint32_t eps_bits, bool gpu_ops);
-// ggml silu on rows of `cols` (Shaders.lean:172-179).
+// ggml silu on rows of `cols` (Shaders.lean:172-179); row tails as soft_max.
 ArrayP silu(const ArrayP &x, int64_t rows, int64_t cols, bool gpu_ops);
 // ggml gelu_erf (Shaders.lean:186-199) with a correctly rounded erff.
 ArrayP gelu_erf(const ArrayP &x, bool tanh_form);
@@ -102,5 +102,11 @@ ArrayP sqrt_exact(const ArrayP &a);
 // Host copy of the product's erff (the same routine the kernels run), for the
 // CPU side of the exhaustive check (c/smlx_shim.c:388-403).
 float erff_host(float x);
+// y[t] = bits(expf(bits^-1(base + t))) with the correctly rounded expf of the
+// row tails (no reference counterpart: the exhaustive check of that expf).
+ArrayP expf_map(uint32_t base, uint32_t count);
+float expf_host(float x);
+// Refuses a row tail (cols % 4 != 0) unless the pinned flavour is selected.
+void require_tail_expf(const char *op, int64_t cols);
 
 }  // namespace shlo

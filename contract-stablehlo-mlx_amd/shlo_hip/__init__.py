@@ -256,6 +256,13 @@ def libm_erff_range(base, count) -> np.ndarray:
     return out
 
 
+def expf_range(base, count) -> np.ndarray:
+    """The row tails' correctly rounded expf on the host, as bit patterns."""
+    out = np.empty(count, dtype=np.uint32)
+    _check(_lib.shlo_expf_range(ctypes.c_uint32(base), ctypes.c_uint32(count), out.ctypes.data_as(_P)))
+    return out
+
+
 class Kernel:
     """A precompiled kernel by name (Kernels/Run.lean's cache of specs)."""
 

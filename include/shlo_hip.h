@@ -110,7 +110,7 @@ int shlo_eval(const shlo_arr *const *xs, size_t n);
 /* ---- precompiled kernels (replacing mx::fast::metal_kernel) --------------- */
 
 /* smlx_kernel_new (c/smlx_shim.c:283-297): resolve `name` ("mul_mat",
- * "soft_max", "norm", "silu", "gelu_erf", "erff_map", "divide", "sqrt",
+ * "soft_max", "norm", "silu", "gelu_erf", "erff_map", "expf_map", "divide", "sqrt",
  * "f64_ew", "f64_of_f32", "f32_of_f64"; an "smlx_" prefix is accepted) to a
  * precompiled gfx950 kernel.  The binding names, source and header of the
  * reference's Metal spec are accepted and ignored (nothing is compiled at run
@@ -204,6 +204,15 @@ int shlo_get_flavor(void);
  * trace.  *prev receives the old value when prev is not NULL.  Not in the
  * reference (mlx compiles to its own graph). */
 int shlo_set_graph_min_ops(int n, int *prev);
+
+/* The correctly rounded expf that ggml's scalar row tails use in the pinned
+ * flavour (soft_max and silu rows with cols % 4 != 0; the stock flavour
+ * refuses them, as the reference does), evaluated on the host over count
+ * consecutive binary32 bit patterns from base, as bit patterns: the CPU side
+ * of its exhaustive check.  The GPU side is the precompiled kernel "expf_map"
+ * (inputs [u32 params: base, count], one u32 output of count words).  Not in
+ * the reference. */
+int shlo_expf_range(uint32_t base, uint32_t count, uint32_t *out);
 
 /* Measurement helpers (not in the reference): a device-side fill from the
  * splitmix32 stream of ref/ggml_ref.c:21-30 — dist 0: unif(a) with a =

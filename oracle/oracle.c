@@ -341,6 +341,17 @@ void orc_erff_range(uint32_t base, uint32_t count, uint32_t *out, int nthreads) 
 	orc_parallel((int64_t)count, nthreads, er_body, &c);
 }
 
+/* The same sweep for the correctly rounded expf (the row tails' expf). */
+static void ex_body(void *p, int64_t lo, int64_t hi) {
+	struct er_ctx *c = (struct er_ctx *)p;
+	for (int64_t i = lo; i < hi; i++) c->out[i] = f2u(orc_expf_cr(u2f(c->base + (uint32_t)i)));
+}
+
+void orc_expf_range(uint32_t base, uint32_t count, uint32_t *out, int nthreads) {
+	struct er_ctx c = { base, out };
+	orc_parallel((int64_t)count, nthreads, ex_body, &c);
+}
+
 uint64_t orc_checksum_words(const uint32_t *w, size_t count, uint64_t start_index) {
 	uint64_t s = 0;
 	for (size_t i = 0; i < count; i++) {

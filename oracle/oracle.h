@@ -106,6 +106,8 @@ void orc_silu(const float *x, float *y, int64_t rows, int64_t cols);
 /* erff over `count` consecutive binary32 bit patterns from `base` (the CPU side
  * of the exhaustive check, Tests/OpTests.lean:273-296). */
 void orc_erff_range(uint32_t base, uint32_t count, uint32_t *out, int nthreads);
+/* orc_expf_cr over count consecutive binary32 patterns from base. */
+void orc_expf_range(uint32_t base, uint32_t count, uint32_t *out, int nthreads);
 
 /* An order-sensitive 64-bit checksum of `count` words: sum over t of
  * (w[t] + 1) * (2t + 1) * 0x9E3779B97F4A7C15 (mod 2^64).  Used to pin the

@@ -140,10 +140,11 @@ def case_names():
     return [_l.orc_case_name(i).decode() for i in range(_l.orc_case_count())]
 
 
-def golden_chunks():
-    """{chunk: checksum} of the exhaustive erff fixture (tests/golden/erff_chunks.txt)."""
+def golden_chunks(fn="erff"):
+    """{chunk: checksum} of an exhaustive fixture (tests/golden/<fn>_chunks.txt:
+    erff, or the row tails' expf)."""
     res = {}
-    with open(os.path.join(ROOT, "tests", "golden", "erff_chunks.txt")) as f:
+    with open(os.path.join(ROOT, "tests", "golden", f"{fn}_chunks.txt")) as f:
         for line in f:
             if line.startswith("#"):
                 continue

@@ -131,6 +131,58 @@ def test_softmax_row_lengths(oracle, cols):
     assert same_bits(got, want)
 
 
+@pytest.mark.parametrize("cols", [1, 2, 3, 5, 7, 13, 257, 1021, 4093, 4095])
+def test_softmax_row_tails_pinned(oracle, cols):
+    """Rows with cols % 4 != 0 in the pinned flavour: the last cols % 4
+    elements through the correctly rounded expf, added after the group parts
+    (with -inf entries, a scale, and the planted binary32 denominator)."""
+    import shlo_hip
+    rows = 37
+    x, _ = oracle.fill_normal(15, 6.0, rows * cols)
+    x = x.reshape(rows, cols)
+    if cols > 2:  # masked entries, never a whole row (NaN bits of -inf - -inf are the platform's)
+        x[np.arange(rows) % 5 == 0, -1] = -np.inf
+        x[np.arange(rows) % 7 == 0, 0] = -np.inf
+    text = custom_call_module("ggml.soft_max", "scale = 0x3F000000 : f32", x.shape)
+    want = oracle.soft_max(x, scale=0.5)
+    shlo_hip.set_flavor(1)
+    try:
+        for compile in (True, False):
+            got = run(text, [x], compile=compile)[0]
+            assert same_bits(got, want), (cols, compile)
+        if cols > 4:
+            got = run(text, [x], faults=shlo_hip.fault_bits("soft_max_float_sum"))[0]
+            assert same_bits(got, oracle.soft_max(x, scale=0.5, float_sum=True))
+    finally:
+        shlo_hip.set_flavor(0)
+
+
+def test_row_tails_refused_in_stock_flavour(oracle):
+    """The stock flavour refuses a row tail, as the reference does
+    (Lower.lean:485-486): its expf is Apple libsystem_m's."""
+    import shlo_hip
+    x, _ = oracle.fill_normal(16, 1.0, 4 * 7)
+    x = x.reshape(4, 7)
+    for target, attrs in (("ggml.soft_max", "scale = 0x3F800000 : f32"), ("ggml.silu", "")):
+        with pytest.raises(shlo_hip.ShloError, match="not carried"):
+            run(custom_call_module(target, attrs, x.shape), [x])
+
+
+@pytest.mark.parametrize("cols", [1, 3, 6, 259, 1023])
+def test_silu_row_tails_pinned(oracle, cols):
+    import shlo_hip
+    rows = 29
+    x, _ = oracle.fill_normal(17, 8.0, rows * cols)
+    x = x.reshape(rows, cols)
+    shlo_hip.set_flavor(1)
+    try:
+        for compile in (True, False):
+            got = run(custom_call_module("ggml.silu", "", x.shape), [x], compile=compile)[0]
+            assert same_bits(got, oracle.silu(x)), (cols, compile)
+    finally:
+        shlo_hip.set_flavor(0)
+
+
 def test_softmax_scale_attribute(oracle):
     x, _ = oracle.fill_normal(12, 8.0, 32 * 256)
     x = x.reshape(32, 256)

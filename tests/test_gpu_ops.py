@@ -101,3 +101,27 @@ def test_erff_map_matches_host_routine():
     y = k.apply([shlo_hip.from_numpy(np.zeros(8, np.float32)), shlo_hip.u32_arr([base, n])], [(n,)], [shlo_hip.U32])[0]
     host = shlo_hip.from_numpy(shlo_hip.libm_erff_range(base, n))
     assert shlo_hip.count_nonzero(shlo_hip.binary("ne", y, host)) == 0
+
+
+def test_expf_exhaustive_on_gpu(oracle):
+    """The row tails' expf on the GPU, all 2^32 inputs, against the
+    MPFR-decided chunk checksums; inputs shifted by one must miss."""
+    import shlo_hip
+    want = oracle.golden_chunks("expf")
+    k = shlo_hip.Kernel("expf_map")
+    bad = []
+    for c in range(256):
+        y = k.apply([shlo_hip.u32_arr([c << 24, 1 << 24])], [(1 << 24,)], [shlo_hip.U32])[0]
+        if shlo_hip.checksum_u32(y, c << 24) != want[c]:
+            bad.append(c)
+    assert bad == []
+    y = k.apply([shlo_hip.u32_arr([(0x3F << 24) + 1, 1 << 24])], [(1 << 24,)], [shlo_hip.U32])[0]
+    assert shlo_hip.checksum_u32(y, 0x3F << 24) != want[0x3F]
+
+
+def test_expf_map_matches_host_routine():
+    import shlo_hip
+    base, n = 0xC2000000, 1 << 22
+    y = shlo_hip.Kernel("expf_map").apply([shlo_hip.u32_arr([base, n])], [(n,)], [shlo_hip.U32])[0]
+    host = shlo_hip.from_numpy(shlo_hip.expf_range(base, n))
+    assert shlo_hip.count_nonzero(shlo_hip.binary("ne", y, host)) == 0
