@@ -465,6 +465,157 @@ static const struct ocase CASES[] = {
 	{ "view_kimodo", OP_VIEW, { 3072, 352, 128, 1024 + 3 * 128 }, 1.0f, 0 },
 };
 
+/* ---- graph.txt: ggml's graph of a case, "ghlo-graph 1" (ggml_ref.c:94-134) --
+ * One line per tensor: the arguments (tensors the nodes read that are not
+ * nodes themselves, in the order the nodes first read them, a view's source
+ * after its srcs), then the nodes in graph order:
+ *   T <i> <op> <unary op or -> <node> <output> <type> <ne0..3> <nb0..3>
+ *     <view source index or -1> <view offset> <src0..9 index or -1> <op_params 0..15>
+ * <op> is ggml_op_name(); a node is an output when no later tensor reads it.
+ * The op_params are ggml's for the ops of these cases: NORM {eps},
+ * SCALE {s, bias 0}, SOFT_MAX {scale 1, max_bias 0}, UNARY {unary op},
+ * CONCAT {dim}, VIEW {byte offset as a size_t}. */
+struct gtensor {
+	const char *op, *un;
+	int node;
+	int64_t ne[4];
+	int64_t nb[4];
+	int view_src;
+	int64_t view_offs;
+	int src[10];
+	int32_t par[16];
+};
+struct graph { struct gtensor t[8]; int n; };
+
+/* ggml_unary_op values at the reference's ggml (GGML_UNARY_OP_SILU, _GELU_ERF); pinned by
+ * the graph.txt hashes of the silu and gelu_erf cases. */
+enum { GGML_UNARY_SILU = 10, GGML_UNARY_GELU_ERF = 16 };
+
+static int gadd(struct graph *g, const char *op, const char *un, int node, int64_t ne0, int64_t ne1, int64_t ne2,
+                int64_t ne3) {
+	struct gtensor *t = &g->t[g->n];
+	memset(t, 0, sizeof *t);
+	t->op = op;
+	t->un = un;
+	t->node = node;
+	t->ne[0] = ne0; t->ne[1] = ne1; t->ne[2] = ne2; t->ne[3] = ne3;
+	t->nb[0] = 4;
+	for (int i = 1; i < 4; i++) t->nb[i] = t->nb[i - 1] * t->ne[i - 1];
+	t->view_src = -1;
+	for (int i = 0; i < 10; i++) t->src[i] = -1;
+	return g->n++;
+}
+
+static int32_t fbits(float f) { int32_t b; memcpy(&b, &f, 4); return b; }
+
+static void build_graph(const struct ocase *c, struct graph *g) {
+	const int64_t *a = c->a;
+	g->n = 0;
+	int x, y, n;
+	switch (c->op) {
+	case OP_MUL_MAT:
+		x = gadd(g, "NONE", "-", 0, a[0], a[1], 1, 1);
+		y = gadd(g, "NONE", "-", 0, a[0], a[2], a[3], 1);
+		n = gadd(g, "MUL_MAT", "-", 1, a[1], a[2], a[3], 1);
+		g->t[n].src[0] = x; g->t[n].src[1] = y;
+		break;
+	case OP_ADD:
+	case OP_MUL:
+		x = gadd(g, "NONE", "-", 0, a[0], a[1], a[2], 1);
+		y = gadd(g, "NONE", "-", 0, a[0], a[1], a[2], 1);
+		n = gadd(g, c->op == OP_ADD ? "ADD" : "MUL", "-", 1, a[0], a[1], a[2], 1);
+		g->t[n].src[0] = x; g->t[n].src[1] = y;
+		break;
+	case OP_REPEAT:
+		x = gadd(g, "NONE", "-", 0, a[0], 1, 1, 1);
+		n = gadd(g, "REPEAT", "-", 1, a[0], a[1], a[2], 1);
+		g->t[n].src[0] = x;
+		break;
+	case OP_NORM:
+		x = gadd(g, "NONE", "-", 0, a[0], a[1], a[2], 1);
+		n = gadd(g, "NORM", "-", 1, a[0], a[1], a[2], 1);
+		g->t[n].src[0] = x; g->t[n].par[0] = fbits(1.e-5f);
+		break;
+	case OP_SCALE:
+		x = gadd(g, "NONE", "-", 0, a[0], a[1], 1, 1);
+		n = gadd(g, "SCALE", "-", 1, a[0], a[1], 1, 1);
+		g->t[n].src[0] = x; g->t[n].par[0] = fbits(1.f / sqrtf(128.0f));
+		break;
+	case OP_SOFT_MAX:
+		x = gadd(g, "NONE", "-", 0, a[0], a[1], 1, 1);
+		n = gadd(g, "SOFT_MAX", "-", 1, a[0], a[1], 1, 1);
+		g->t[n].src[0] = x; g->t[n].par[0] = fbits(1.0f);
+		break;
+	case OP_GELU:
+	case OP_SILU:
+		x = gadd(g, "NONE", "-", 0, a[0], a[1], a[2], 1);
+		n = gadd(g, "UNARY", c->op == OP_GELU ? "GELU_ERF" : "SILU", 1, a[0], a[1], a[2], 1);
+		g->t[n].src[0] = x; g->t[n].par[0] = c->op == OP_GELU ? GGML_UNARY_GELU_ERF : GGML_UNARY_SILU;
+		break;
+	case OP_CONCAT: {
+		const int dim = (int)a[0];
+		int64_t bn[3] = { a[1], a[2], a[3] }, on[3] = { a[1], a[2], a[3] };
+		bn[dim] = a[4];
+		on[dim] += a[4];
+		x = gadd(g, "NONE", "-", 0, a[1], a[2], a[3], 1);
+		y = gadd(g, "NONE", "-", 0, bn[0], bn[1], bn[2], 1);
+		n = gadd(g, "CONCAT", "-", 1, on[0], on[1], on[2], 1);
+		g->t[n].src[0] = x; g->t[n].src[1] = y; g->t[n].par[0] = dim;
+		break;
+	}
+	case OP_TRANSPOSE: {  /* cont(transpose(x)): the transpose is a view of x with ne and nb swapped */
+		x = gadd(g, "NONE", "-", 0, a[0], a[1], 1, 1);
+		const int v = gadd(g, "TRANSPOSE", "-", 1, a[1], a[0], 1, 1);
+		struct gtensor *t = &g->t[v];
+		t->nb[0] = g->t[x].nb[1]; t->nb[1] = g->t[x].nb[0]; t->nb[2] = g->t[x].nb[2]; t->nb[3] = g->t[x].nb[3];
+		t->view_src = x; t->src[0] = x;
+		n = gadd(g, "CONT", "-", 1, a[1], a[0], 1, 1);
+		g->t[n].src[0] = v;
+		break;
+	}
+	case OP_VIEW: {  /* cont(view_2d(x, hw, seq, x->nb[1], off * 4)) */
+		const int64_t W = a[0], S = a[1], HW = a[2], off = a[3] * 4;
+		x = gadd(g, "NONE", "-", 0, W, S, 1, 1);
+		const int v = gadd(g, "VIEW", "-", 1, HW, S, 1, 1);
+		struct gtensor *t = &g->t[v];
+		t->nb[1] = g->t[x].nb[1]; t->nb[2] = t->nb[1] * S; t->nb[3] = t->nb[2];
+		t->view_src = x; t->view_offs = off; t->src[0] = x;
+		t->par[0] = (int32_t)(uint32_t)(uint64_t)off; t->par[1] = (int32_t)(uint32_t)((uint64_t)off >> 32);
+		n = gadd(g, "CONT", "-", 1, HW, S, 1, 1);
+		g->t[n].src[0] = v;
+		break;
+	}
+	}
+}
+
+static int wgraph(struct writer *w, const struct ocase *c) {
+	struct graph g;
+	build_graph(c, &g);
+	char p[1200];
+	snprintf(p, sizeof p, "%s/graph.txt", w->dir);
+	FILE *f = fopen(p, "w");
+	if (!f) return -2;
+	fprintf(f, "ghlo-graph 1\n");
+	for (int i = 0; i < g.n; i++) {
+		const struct gtensor *t = &g.t[i];
+		int output = 0;
+		if (t->node) {
+			int used = 0;
+			for (int j = i + 1; j < g.n; j++)
+				for (int s = 0; s < 10; s++) used |= g.t[j].src[s] == i || g.t[j].view_src == i;
+			output = !used;
+		}
+		fprintf(f, "T %d %s %s %d %d f32 %lld %lld %lld %lld %lld %lld %lld %lld %d %lld", i, t->op, t->un, t->node,
+		        output, (long long)t->ne[0], (long long)t->ne[1], (long long)t->ne[2], (long long)t->ne[3],
+		        (long long)t->nb[0], (long long)t->nb[1], (long long)t->nb[2], (long long)t->nb[3], t->view_src,
+		        (long long)t->view_offs);
+		for (int s = 0; s < 10; s++) fprintf(f, " %d", t->src[s]);
+		for (int q = 0; q < 16; q++) fprintf(f, " %d", t->par[q]);
+		fprintf(f, "\n");
+	}
+	return fclose(f) ? -2 : 0;
+}
+
 int orc_case_count(void) { return (int)(sizeof CASES / sizeof CASES[0]); }
 const char *orc_case_name(int i) { return i >= 0 && i < orc_case_count() ? CASES[i].name : NULL; }
 
@@ -590,6 +741,7 @@ int orc_write_case(const char *outdir, const char *name, int pinned) {
 	}
 	}
 	int rc = wfinish(&w, &out);
+	if (rc == 0) rc = wgraph(&w, c);
 	free(t0.d);
 	free(t1.d);
 	free(out.d);

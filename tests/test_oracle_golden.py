@@ -1,8 +1,8 @@
 """The oracle against the reference's golden vectors and against mathematics.
 
-The reference's fixtures are the SHA-256 hashes of every input and output
-ref/ggml_ref.c writes (evidence/ref-pinned.sha256, ref-stock.sha256, copied
-under tests/golden/).  The oracle must regenerate all of them; each check
+The reference's fixtures are the SHA-256 hashes of every input, output and
+graph.txt ref/ggml_ref.c writes (evidence/ref-pinned.sha256, ref-stock.sha256,
+copied under tests/golden/).  The oracle must regenerate all of them; each check
 below also has a planted mistake (made in the oracle, on the CPU) that it
 must catch.
 """
@@ -15,12 +15,14 @@ import pytest
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 
 
-def _hashes(flavor):
+def _hashes(flavor, graphs=False):
+    """path -> SHA-256 of the reference's in*.f32 / out.f32 files, or of its
+    graph.txt files (ggml's graph per case, "ghlo-graph 1") with graphs=True."""
     res = {}
     with open(os.path.join(ROOT, "tests", "golden", f"ref-{flavor}.sha256")) as f:
         for line in f:
             h, p = line.split()
-            if not p.endswith("graph.txt"):
+            if p.endswith("graph.txt") == graphs:
                 res[p] = h
     return res
 
@@ -38,6 +40,27 @@ def test_pinned_fixtures_bit_exact(ref_pinned):
     """Every in*.f32 and out.f32 of the pinned reference build (96 files)."""
     assert len(_hashes("pinned")) == 96
     assert _mismatches(ref_pinned, "pinned") == []
+
+
+@pytest.mark.parametrize("flavor", ["pinned", "stock"])
+def test_graph_descriptions_bit_exact(ref_pinned, ref_stock, flavor):
+    """Every case's graph.txt (ggml's graph as contract-ggml-stablehlo's backend
+    describes it, ref/ggml_ref.c:94-134): 38 files per flavour, the same in both."""
+    ref = ref_pinned if flavor == "pinned" else ref_stock
+    want = _hashes(flavor, graphs=True)
+    assert len(want) == 38
+    assert sorted(p for p, h in want.items() if _sha(os.path.join(ref, p)) != h) == []
+
+
+def test_graph_description_catches_a_wrong_op_param(ref_pinned):
+    """A planted mistake: the GELU_ERF unary op code one off changes the hash."""
+    p = os.path.join(ref_pinned, "gelu_erf_small", "graph.txt")
+    lines = open(p).read().splitlines()
+    w = lines[2].split()
+    assert w[2:4] == ["UNARY", "GELU_ERF"]
+    w[27] = str(int(w[27]) - 1)
+    text = "\n".join(lines[:2] + [" ".join(w)]) + "\n"
+    assert hashlib.sha256(text.encode()).hexdigest() != _hashes("pinned", graphs=True)["gelu_erf_small/graph.txt"]
 
 
 def test_stock_fixtures_bit_exact_except_platform_erff(ref_stock):
