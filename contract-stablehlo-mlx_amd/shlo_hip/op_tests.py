@@ -20,7 +20,7 @@ import time
 import numpy as np
 
 from . import (F32, FAULTS, Module, ShloError, U32, binary, count_nonzero, fault_bits, from_numpy, get_flavor,
-               libm_erff_range, Kernel, u32_arr, unary)
+               libm_erff_range, Kernel, set_flavor, u32_arr, unary)
 
 
 def ty_of(ne):
@@ -324,10 +324,94 @@ def erff_exhaustive(t: Tally, chunk_log=24):
     t.note(nz != 0, f"erff_exhaustive planted fault (reference shifted by one input): {nz} of {chunk} differ (must be > 0)")
 
 
+# ---- the generic path: each case's graph.txt through the graph emitter ---------------
+
+# The executor's planted faults a generic module can be broken with, first match
+# wins (OpTests.lean:339-349), then the ggml.* kernels' own.
+_GHLO_FAULTS = [
+    ('"stablehlo.add"', "binary_half", "float16 arithmetic"),
+    ('"stablehlo.multiply"', "binary_half", "float16 arithmetic"),
+    ('"stablehlo.concatenate"', "concat_swap", "operands swapped"),
+    ('"stablehlo.transpose"', "transpose_identity", "no permutation"),
+    ('"stablehlo.slice"', "slice_shift", "offset one late"),
+    ('"stablehlo.broadcast_in_dim"', "broadcast_first", "broadcast of the first element"),
+    ('"stablehlo.dot_general"', "dot_builtin", "built-in matmul"),
+    ('"ggml.soft_max"', "soft_max_float_sum", "binary32 denominator"),
+    ('"ggml.norm"', "norm_gpu_ops", "binary32 sums and GPU / and sqrt"),
+    ('"ggml.gelu_erf"', "gelu_tanh", "tanh-form GELU"),
+    ('"ggml.silu"', "silu_gpu_ops", "GPU exp and /"),
+]
+
+
+def ghlo_case(ref, t: Tally, name, expect_refusal=False):
+    """OpTests.ghloCase (OpTests.lean:303-359) over graph.txt: the case's graph
+    emitted as a generic module (a leading ui64 0, rank-4 tensors), run
+    compiled, compared with out.f32, then run with a planted executor fault
+    that must change it."""
+    from . import ghlo
+    d = os.path.join(ref, name)
+    gp = os.path.join(d, "graph.txt")
+    if not os.path.exists(gp):
+        t.note(False, f"ghlo {name}: graph missing ({gp})")
+        return
+    try:
+        text, args, outs = ghlo.emit(open(gp).read())
+    except ghlo.GraphError as e:
+        t.note(False, f"ghlo {name}: not emitted: {e}")
+        return
+    md = read_meta(d)
+    in_meta = [(n, ne) for n, ne in md if n.startswith("in")]
+    if len(in_meta) != len(args):
+        t.note(False, f"ghlo {name}: module takes {len(args)} tensors, the case has {len(in_meta)}")
+        return
+    ins = [from_numpy(np.zeros((), np.uint64))]
+    for n, ne in in_meta:
+        ins.append(from_numpy(np.fromfile(os.path.join(d, f"{n}.f32"), dtype=np.float32)
+                              .reshape(ne[3], ne[2], ne[1], ne[0])))
+    with open(os.path.join(d, "out.f32"), "rb") as f:
+        want = f.read()
+    count = len(want) // 4
+    t0 = time.perf_counter()
+    ok, r = run_module(text, ins, 0, True)
+    ms = (time.perf_counter() - t0) * 1e3
+    if expect_refusal:
+        t.note(not ok and "not carried" in r, f"ghlo {name}: refused as expected: {r[:160]}" if not ok else
+               f"ghlo {name}: ran, but it reaches code this executor does not carry")
+        return
+    if not ok:
+        t.note(False, f"ghlo {name}: did not run: {r[:300]}")
+        return
+    n, first = diff(r, want)
+    detail = f" first at {first}: got {hex32(word(r, first))} want {hex32(word(want, first))}" if first is not None else ""
+    t.note(n == 0, f"ghlo {name}: {n} of {count} words differ{detail} ({ms:.3f} ms incl. trace)")
+    pick = next(((f, fn) for key, f, fn in _GHLO_FAULTS if key in text), None)
+    if pick is not None and pick[0] == "dot_builtin" and get_flavor() == 0:
+        # The stock tail with K < 4 is exactly the natural-order FMA chain of the
+        # built-in matmul; the unfused sequential sum differs from it for K >= 2.
+        pick = ("dot_plain", "sequential sum without FMA")
+    if pick is None:
+        t.note(False, f"ghlo {name}: no executor fault applies to this module")
+        return
+    ok, r = run_module(text, ins, fault_bits(pick[0]), True)
+    if not ok:
+        t.note(True, f"ghlo {name} executor fault ({pick[1]}): refused: {r[:100]}")
+    else:
+        n, _ = diff(r, want)
+        t.note(n != 0, f"ghlo {name} executor fault ({pick[1]}): {n} of {count} differ (must be > 0)")
+
+
 def main(argv=None):
     argv = list(sys.argv[1:] if argv is None else argv)
+    pinned = None
+    if "--pinned" in argv:
+        k = argv.index("--pinned")
+        if k + 1 >= len(argv):
+            print("--pinned needs a directory", file=sys.stderr)
+            return 2
+        pinned = argv[k + 1]
+        argv = argv[:k] + argv[k + 2:]
     if not argv:
-        print("usage: python -m shlo_hip.op_tests <ref-dir> [case ...]", file=sys.stderr)
+        print("usage: python -m shlo_hip.op_tests <ref-dir> [--pinned <pinned-ref-dir>] [case ...]", file=sys.stderr)
         return 2
     ref, only = argv[0], argv[1:]
     want = lambda n: not only or n in only
@@ -337,6 +421,15 @@ def main(argv=None):
     for c in CASES:
         if want(c.name):
             run_case(ref, t, c)
+    if pinned is not None:  # the generic path, pinned flavour (OpTests.lean:369-372)
+        prev = get_flavor()
+        set_flavor(1)
+        try:
+            for c in CASES:
+                if want(c.name):
+                    ghlo_case(pinned, t, c.name)
+        finally:
+            set_flavor(prev)
     if want("erff_exhaustive"):
         erff_exhaustive(t)
     print(f"\n{t.passed} passed, {t.failed} failed")
