@@ -39,4 +39,27 @@ __host__ __device__ inline float ggml_v_expf(float x) {
   return an > bits_f(0x43400000u) ? big : (an > bits_f(0x42FC0000u) ? mid : nrm);
 }
 
+// ggml_v_expf for arguments that are <= 0, -inf or NaN (a softmax row minus
+// its maximum), with the same bits: there the |n| > 192 branch gives exactly
+// +0 (2^-125 squared underflows), so only the 126 < |n| <= 192 branch needs its
+// own formula.  *mid is set when x falls in that branch; the caller then
+// recomputes x with ggml_v_expf.
+__host__ __device__ inline float ggml_v_expf_nonpos(float x, bool *mid) {
+  const float r = bits_f(0x4B400000u);
+  const float z = __builtin_fmaf(x, bits_f(0x3FB8AA3Bu), r);
+  const float n = z - r;
+  const float b = __builtin_fmaf(-n, bits_f(0x35BFBE8Eu), __builtin_fmaf(-n, bits_f(0x3F317200u), x));
+  const uint32_t e = f_bits(z) << 23;
+  const float k = bits_f(e + 0x3F800000u);
+  const float u = b * b;
+  const float p1 = __builtin_fmaf(bits_f(0x3E2AAF33u), b, bits_f(0x3EFFFEDBu));
+  const float p2 = __builtin_fmaf(bits_f(0x3C072010u), b, bits_f(0x3D2B9F17u));
+  const float p3 = __builtin_fmaf(p2, u, p1);
+  const float j = __builtin_fmaf(p3, u, bits_f(0x3F7FFFF6u) * b);
+  const float an = __builtin_fabsf(n);
+  const bool big = an > bits_f(0x43400000u);
+  *mid = !big && an > bits_f(0x42FC0000u);
+  return big ? 0.0f : __builtin_fmaf(k, j, k);
+}
+
 }  // namespace shlo

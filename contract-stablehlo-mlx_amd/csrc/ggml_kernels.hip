@@ -389,16 +389,39 @@ __global__ void __launch_bounds__(256) soft_max_rows_k(int64_t rows, int cols, f
       const float other = __shfl_xor(mx, o, kWave);
       mx = mx > other ? mx : other;
     }
+    // The arguments x*sc - mx are <= 0 (or -inf, or NaN): the fast form, with
+    // the rare 126 < |n| <= 192 elements recomputed when any lane has one.
+    float4 v[J];
+    bool mid = false;
 #pragma unroll
     for (int j = 0; j < J; j++) {
       const int g = lane + kWave * j;
       if (g < G) {
-        e[rr][j].x = ggml_v_expf(e[rr][j].x * sc - mx);
-        e[rr][j].y = ggml_v_expf(e[rr][j].y * sc - mx);
-        e[rr][j].z = ggml_v_expf(e[rr][j].z * sc - mx);
-        e[rr][j].w = ggml_v_expf(e[rr][j].w * sc - mx);
-        parts[lr * PS + g] = (double)((e[rr][j].x + e[rr][j].y) + (e[rr][j].z + e[rr][j].w));
+        bool m0, m1, m2, m3;
+        v[j] = make_float4(e[rr][j].x * sc - mx, e[rr][j].y * sc - mx, e[rr][j].z * sc - mx, e[rr][j].w * sc - mx);
+        e[rr][j].x = ggml_v_expf_nonpos(v[j].x, &m0);
+        e[rr][j].y = ggml_v_expf_nonpos(v[j].y, &m1);
+        e[rr][j].z = ggml_v_expf_nonpos(v[j].z, &m2);
+        e[rr][j].w = ggml_v_expf_nonpos(v[j].w, &m3);
+        mid |= m0 | m1 | m2 | m3;
       }
+    }
+    if (__any(mid)) {
+#pragma unroll
+      for (int j = 0; j < J; j++) {
+        const int g = lane + kWave * j;
+        if (g < G) {
+          e[rr][j].x = ggml_v_expf(v[j].x);
+          e[rr][j].y = ggml_v_expf(v[j].y);
+          e[rr][j].z = ggml_v_expf(v[j].z);
+          e[rr][j].w = ggml_v_expf(v[j].w);
+        }
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < J; j++) {
+      const int g = lane + kWave * j;
+      if (g < G) parts[lr * PS + g] = (double)((e[rr][j].x + e[rr][j].y) + (e[rr][j].z + e[rr][j].w));
     }
   }
   __syncthreads();

@@ -131,6 +131,24 @@ def test_softmax_row_lengths(oracle, cols):
     assert same_bits(got, want)
 
 
+@pytest.mark.parametrize("cols", [256, 1024, 4096])
+def test_softmax_subnormal_exps(oracle, cols):
+    """Rows whose entries sit 80-140 below the row maximum: ggml_v_expf's
+    126 < |n| <= 192 branch (subnormal results) and the |n| > 192 branch (+0),
+    with -inf entries, next to ordinary ones."""
+    rng = np.random.default_rng(cols)
+    rows = 64
+    x = rng.uniform(-140.0, -80.0, (rows, cols)).astype(np.float32)
+    x[:, 0] = 0.0
+    x[::3, 1:cols // 4] = rng.normal(0, 2, (len(range(0, rows, 3)), cols // 4 - 1)).astype(np.float32)
+    x[::5, -7:] = -np.inf
+    x[::7, 2:9] = -250.0
+    want = oracle.soft_max(x)
+    got = run(custom_call_module("ggml.soft_max", "scale = 0x3F800000 : f32", x.shape), [x])[0]
+    assert same_bits(got, want)
+    assert np.any((got > 0) & (got < np.float32(1.1754944e-38)))  # subnormal outputs reached
+
+
 @pytest.mark.parametrize("cols", [1, 2, 3, 5, 7, 13, 257, 1021, 4093, 4095])
 def test_softmax_row_tails_pinned(oracle, cols):
     """Rows with cols % 4 != 0 in the pinned flavour: the last cols % 4
