@@ -345,7 +345,9 @@ __host__ __device__ inline int softmax_rows_part_stride(int G) { return (G + 1) 
 // row per row.  Then lane r of wave 0 runs row r's binary64 sum over the parts
 // in group order, so one v_add_f64 advances 4*RPW rows; the other waves wait
 // at the barrier.  Finally every wave scales and stores.
-template <int J, int RPW>
+// FULL: every lane owns exactly J groups (cols == 256*J), so no group index
+// needs a bounds check.
+template <int J, int RPW, bool FULL>
 __global__ void __launch_bounds__(256) soft_max_rows_k(int64_t rows, int cols, float sc, int float_sum,
                                                        const float *__restrict__ X, float *__restrict__ Y) {
   extern __shared__ double lds_d[];
@@ -365,7 +367,7 @@ __global__ void __launch_bounds__(256) soft_max_rows_k(int64_t rows, int cols, f
 #pragma unroll
     for (int j = 0; j < J; j++) {
       const int g = lane + kWave * j;
-      if (g < G) e[rr][j] = ld4_nt(x + 4 * g);
+      if (FULL || g < G) e[rr][j] = ld4_nt(x + 4 * g);
     }
   }
 #pragma unroll
@@ -376,7 +378,7 @@ __global__ void __launch_bounds__(256) soft_max_rows_k(int64_t rows, int cols, f
 #pragma unroll
     for (int j = 0; j < J; j++) {
       const int g = lane + kWave * j;
-      if (g < G) {
+      if (FULL || g < G) {
         const float w0 = e[rr][j].x * sc, w1 = e[rr][j].y * sc, w2 = e[rr][j].z * sc, w3 = e[rr][j].w * sc;
         mx = mx > w0 ? mx : w0;
         mx = mx > w1 ? mx : w1;
@@ -396,7 +398,7 @@ __global__ void __launch_bounds__(256) soft_max_rows_k(int64_t rows, int cols, f
 #pragma unroll
     for (int j = 0; j < J; j++) {
       const int g = lane + kWave * j;
-      if (g < G) {
+      if (FULL || g < G) {
         bool m0, m1, m2, m3;
         v[j] = make_float4(e[rr][j].x * sc - mx, e[rr][j].y * sc - mx, e[rr][j].z * sc - mx, e[rr][j].w * sc - mx);
         e[rr][j].x = ggml_v_expf_nonpos(v[j].x, &m0);
@@ -410,7 +412,7 @@ __global__ void __launch_bounds__(256) soft_max_rows_k(int64_t rows, int cols, f
 #pragma unroll
       for (int j = 0; j < J; j++) {
         const int g = lane + kWave * j;
-        if (g < G) {
+        if (FULL || g < G) {
           e[rr][j].x = ggml_v_expf(v[j].x);
           e[rr][j].y = ggml_v_expf(v[j].y);
           e[rr][j].z = ggml_v_expf(v[j].z);
@@ -421,7 +423,7 @@ __global__ void __launch_bounds__(256) soft_max_rows_k(int64_t rows, int cols, f
 #pragma unroll
     for (int j = 0; j < J; j++) {
       const int g = lane + kWave * j;
-      if (g < G) parts[lr * PS + g] = (double)((e[rr][j].x + e[rr][j].y) + (e[rr][j].z + e[rr][j].w));
+      if (FULL || g < G) parts[lr * PS + g] = (double)((e[rr][j].x + e[rr][j].y) + (e[rr][j].z + e[rr][j].w));
     }
   }
   __syncthreads();
@@ -448,7 +450,7 @@ __global__ void __launch_bounds__(256) soft_max_rows_k(int64_t rows, int cols, f
 #pragma unroll
     for (int j = 0; j < J; j++) {
       const int g = lane + kWave * j;
-      if (g < G) st4_nt(y + 4 * g, make_float4(e[rr][j].x * inv, e[rr][j].y * inv, e[rr][j].z * inv, e[rr][j].w * inv));
+      if (FULL || g < G) st4_nt(y + 4 * g, make_float4(e[rr][j].x * inv, e[rr][j].y * inv, e[rr][j].z * inv, e[rr][j].w * inv));
     }
   }
 }
@@ -1018,16 +1020,21 @@ ArrayP soft_max(const ArrayP &x0, int64_t rows, int64_t cols, uint32_t scale_bit
   const int64_t nblk = (rows + 4 * RPW - 1) / (4 * RPW);
   if (nblk > 0x7FFFFFFF) fail("ggml.soft_max: too many rows");
   const unsigned grid = (unsigned)nblk;
+  const bool full = cols == 4LL * kWave * J;
   launch([=](hipStream_t s) {
     (void)kx;
 #define SM_CASE(n)                                                                                  \
   case n:                                                                                           \
-    if (RPW == 4) soft_max_rows_k<n, 4><<<grid, 256, lds, s>>>(rows, c, sc, fs, px, py);            \
-    else if (RPW == 2) soft_max_rows_k<n, 2><<<grid, 256, lds, s>>>(rows, c, sc, fs, px, py);       \
-    else soft_max_rows_k<n, 1><<<grid, 256, lds, s>>>(rows, c, sc, fs, px, py);                     \
+    if (RPW == 4) soft_max_rows_k<n, 4, false><<<grid, 256, lds, s>>>(rows, c, sc, fs, px, py);     \
+    else if (RPW == 2) soft_max_rows_k<n, 2, false><<<grid, 256, lds, s>>>(rows, c, sc, fs, px, py);\
+    else if (full) soft_max_rows_k<n, 1, true><<<grid, 256, lds, s>>>(rows, c, sc, fs, px, py);     \
+    else soft_max_rows_k<n, 1, false><<<grid, 256, lds, s>>>(rows, c, sc, fs, px, py);              \
     break;
-#define SM_CASE1(n) \
-  case n: soft_max_rows_k<n, 1><<<grid, 256, lds, s>>>(rows, c, sc, fs, px, py); break;
+#define SM_CASE1(n)                                                                                 \
+  case n:                                                                                           \
+    if (full) soft_max_rows_k<n, 1, true><<<grid, 256, lds, s>>>(rows, c, sc, fs, px, py);          \
+    else soft_max_rows_k<n, 1, false><<<grid, 256, lds, s>>>(rows, c, sc, fs, px, py);              \
+    break;
     switch (J) {
       SM_CASE(1) SM_CASE(2) SM_CASE(3) SM_CASE(4) SM_CASE1(5) SM_CASE1(6) SM_CASE1(7) SM_CASE1(8)
       SM_CASE1(9) SM_CASE1(10) SM_CASE1(11) SM_CASE1(12) SM_CASE1(13) SM_CASE1(14) SM_CASE1(15) SM_CASE1(16)
