@@ -346,8 +346,14 @@ __host__ __device__ inline int softmax_rows_part_stride(int G) { return (G + 1) 
 // in group order, so one v_add_f64 advances 4*RPW rows; the other waves wait
 // at the barrier.  Finally every wave scales and stores.
 // FULL: every lane owns exactly J groups (cols == 256*J), so no group index
-// needs a bounds check.
-template <int J, int RPW, bool FULL>
+// needs a bounds check.  UNIT: scale == 1, so x*sc is x (a NaN x makes the
+// whole row NaN either way, through its own part of the sum).
+//
+// The row maximum uses v_max_f32.  On rows without NaN it equals ggml's
+// (mx > w ? mx : w) chain in any order (a +0/-0 tie cannot change an
+// output); a NaN anywhere in a row makes every output NaN through the sum,
+// whatever the maximum.
+template <int J, int RPW, bool FULL, bool UNIT = false>
 __global__ void __launch_bounds__(256) soft_max_rows_k(int64_t rows, int cols, float sc, int float_sum,
                                                        const float *__restrict__ X, float *__restrict__ Y) {
   extern __shared__ double lds_d[];
@@ -379,18 +385,13 @@ __global__ void __launch_bounds__(256) soft_max_rows_k(int64_t rows, int cols, f
     for (int j = 0; j < J; j++) {
       const int g = lane + kWave * j;
       if (FULL || g < G) {
-        const float w0 = e[rr][j].x * sc, w1 = e[rr][j].y * sc, w2 = e[rr][j].z * sc, w3 = e[rr][j].w * sc;
-        mx = mx > w0 ? mx : w0;
-        mx = mx > w1 ? mx : w1;
-        mx = mx > w2 ? mx : w2;
-        mx = mx > w3 ? mx : w3;
+        if (!UNIT) e[rr][j] = make_float4(e[rr][j].x * sc, e[rr][j].y * sc, e[rr][j].z * sc, e[rr][j].w * sc);
+        mx = __builtin_fmaxf(mx, __builtin_fmaxf(__builtin_fmaxf(e[rr][j].x, e[rr][j].y),
+                                                 __builtin_fmaxf(e[rr][j].z, e[rr][j].w)));
       }
     }
 #pragma unroll
-    for (int o = 32; o > 0; o >>= 1) {
-      const float other = __shfl_xor(mx, o, kWave);
-      mx = mx > other ? mx : other;
-    }
+    for (int o = 32; o > 0; o >>= 1) mx = __builtin_fmaxf(mx, __shfl_xor(mx, o, kWave));
     // The arguments x*sc - mx are <= 0 (or -inf, or NaN): the fast form, with
     // the rare 126 < |n| <= 192 elements recomputed when any lane has one.
     float4 v[J];
@@ -400,7 +401,7 @@ __global__ void __launch_bounds__(256) soft_max_rows_k(int64_t rows, int cols, f
       const int g = lane + kWave * j;
       if (FULL || g < G) {
         bool m0, m1, m2, m3;
-        v[j] = make_float4(e[rr][j].x * sc - mx, e[rr][j].y * sc - mx, e[rr][j].z * sc - mx, e[rr][j].w * sc - mx);
+        v[j] = make_float4(e[rr][j].x - mx, e[rr][j].y - mx, e[rr][j].z - mx, e[rr][j].w - mx);  // e holds x*sc
         e[rr][j].x = ggml_v_expf_nonpos(v[j].x, &m0);
         e[rr][j].y = ggml_v_expf_nonpos(v[j].y, &m1);
         e[rr][j].z = ggml_v_expf_nonpos(v[j].z, &m2);
@@ -1021,12 +1022,14 @@ ArrayP soft_max(const ArrayP &x0, int64_t rows, int64_t cols, uint32_t scale_bit
   if (nblk > 0x7FFFFFFF) fail("ggml.soft_max: too many rows");
   const unsigned grid = (unsigned)nblk;
   const bool full = cols == 4LL * kWave * J;
+  const bool unit = scale_bits == 0x3F800000u;
   launch([=](hipStream_t s) {
     (void)kx;
 #define SM_CASE(n)                                                                                  \
   case n:                                                                                           \
     if (RPW == 4) soft_max_rows_k<n, 4, false><<<grid, 256, lds, s>>>(rows, c, sc, fs, px, py);     \
     else if (RPW == 2) soft_max_rows_k<n, 2, false><<<grid, 256, lds, s>>>(rows, c, sc, fs, px, py);\
+    else if (full && unit) soft_max_rows_k<n, 1, true, true><<<grid, 256, lds, s>>>(rows, c, sc, fs, px, py); \
     else if (full) soft_max_rows_k<n, 1, true><<<grid, 256, lds, s>>>(rows, c, sc, fs, px, py);     \
     else soft_max_rows_k<n, 1, false><<<grid, 256, lds, s>>>(rows, c, sc, fs, px, py);              \
     break;
