@@ -127,19 +127,22 @@ __global__ void __launch_bounds__(256) dot_ggml_simple(int64_t n_out, int64_t N,
 // serial tail run per output, exactly as in dot_finish.
 //
 // Workgroup: 4 waves on a 64 (n) x 64 (m) output tile; operands staged in LDS
-// as [row][k] (row stride KC + 4 floats), KC = 64 (four k-blocks) per stage,
-// double-buffered, the next stage prefetched into registers while the matrix
-// cores work on the current one.
+// as [row][k] (row stride KC + 4 floats), KC = 128 (eight k-blocks) per stage,
+// double-buffered (135 KB of gfx950's 160 KB), the next stage prefetched into
+// registers while the matrix cores work on the current one.
 
 typedef float v32f __attribute__((ext_vector_type(32)));
 
 constexpr int kMT = 64;        // tile rows (n) and columns (m)
-constexpr int kKC = 64;        // k per stage
-constexpr int kLS = kKC + 4;   // LDS row stride (floats)
+constexpr int kKC = 128;       // k per stage (8 blocks of 16)
+constexpr int kLS = kKC + 4;   // LDS row stride (floats): rows start 4 banks apart
+constexpr int kRegs = kMT * kKC / 4 / 256;  // float4 per thread per operand per stage
 
 // How an operand tile is loaded: kLoadRowVec = rows contiguous in k (sk == 1),
-// float4 along k; kLoadColVec = free dim contiguous (sf == 1), float4 along the
-// free dim, transposed into LDS; kLoadScalar = any strides.
+// float4 along k; kLoadColVec = free dim contiguous (sf == 1), four scalar
+// loads per thread (four consecutive k of one row, each load coalesced across
+// the wave along the free dim); kLoadScalar = any strides.  Every thread then
+// writes 16-byte [row][k] chunks to LDS.
 enum { kLoadRowVec = 0, kLoadColVec = 1, kLoadScalar = 2 };
 
 struct MfmaOperand {
@@ -148,21 +151,28 @@ struct MfmaOperand {
   int64_t rows;  // N or M
 };
 
-// Stage s of one operand into registers: 4096 floats per tile, 16 per thread.
+// Stage s of one operand into registers: kMT * kKC floats per tile.
 template <int LOAD>
-__device__ __forceinline__ void mfma_fetch(const MfmaOperand &o, int64_t b, int64_t r0, int s, int nb, float4 (&reg)[4]) {
+__device__ __forceinline__ void mfma_fetch(const MfmaOperand &o, int64_t b, int64_t r0, int s, int nb,
+                                           float4 (&reg)[kRegs]) {
   const int t = threadIdx.x;
 #pragma unroll
-  for (int i = 0; i < 4; i++) {
+  for (int i = 0; i < kRegs; i++) {
     const int f = t + 256 * i;
     if (LOAD == kLoadColVec) {
-      const int kr = f / 16, rq = (f % 16) * 4;
-      const int k = s * kKC + kr;
-      int64_t row = r0 + rq;
-      if (row > o.rows - 4) row = o.rows - 4;  // stays in bounds; those outputs are discarded
-      if (k / 16 < nb) reg[i] = ld4(o.p + b * o.sb + row + (int64_t)k * o.sk);
+      // Lane-consecutive rows (the contiguous free dim, so each of the four
+      // loads is coalesced across the wave), four consecutive k per thread:
+      // the thread then writes one 16-byte [row][k] chunk to LDS.
+      const int row_l = f % kMT, kq = (f / kMT) * 4;
+      const int k = s * kKC + kq;
+      int64_t row = r0 + row_l;
+      if (row > o.rows - 1) row = o.rows - 1;  // stays in bounds; those outputs are discarded
+      if (k / 16 < nb) {
+        const float *q = o.p + b * o.sb + row + (int64_t)k * o.sk;
+        reg[i] = make_float4(q[0], q[o.sk], q[2 * o.sk], q[3 * o.sk]);
+      }
     } else {
-      const int row_l = f / 16, kq = (f % 16) * 4;
+      const int row_l = f / (kKC / 4), kq = (f % (kKC / 4)) * 4;
       const int k = s * kKC + kq;
       int64_t row = r0 + row_l;
       if (row > o.rows - 1) row = o.rows - 1;
@@ -180,28 +190,39 @@ __device__ __forceinline__ void mfma_fetch(const MfmaOperand &o, int64_t b, int6
 }
 
 template <int LOAD>
-__device__ __forceinline__ void mfma_stash(float *lds, const float4 (&reg)[4]) {
+__device__ __forceinline__ void mfma_stash(float *lds, const float4 (&reg)[kRegs]) {
   const int t = threadIdx.x;
 #pragma unroll
-  for (int i = 0; i < 4; i++) {
+  for (int i = 0; i < kRegs; i++) {
     const int f = t + 256 * i;
     if (LOAD == kLoadColVec) {
-      const int kr = f / 16, rq = (f % 16) * 4;
-      lds[(rq + 0) * kLS + kr] = reg[i].x;
-      lds[(rq + 1) * kLS + kr] = reg[i].y;
-      lds[(rq + 2) * kLS + kr] = reg[i].z;
-      lds[(rq + 3) * kLS + kr] = reg[i].w;
+      const int row_l = f % kMT, kq = (f / kMT) * 4;
+      st4(lds + row_l * kLS + kq, reg[i]);  // rows 68 floats apart: 16 lanes, 16 distinct bank quads
     } else {
-      const int row_l = f / 16, kq = (f % 16) * 4;
+      const int row_l = f / (kKC / 4), kq = (f % (kKC / 4)) * 4;
       st4(lds + row_l * kLS + kq, reg[i]);
     }
   }
 }
 
+// One k-block of 16: the 8 fused multiply-adds per output, residues q and q+8.
+__device__ __forceinline__ void mfma_block(v32f (&acc)[8], const float4 &a0, const float4 &a1, const float4 &b0,
+                                           const float4 &b1) {
+  acc[0] = __builtin_amdgcn_mfma_f32_32x32x1f32(a0.x, b0.x, acc[0], 0, 0, 0);
+  acc[1] = __builtin_amdgcn_mfma_f32_32x32x1f32(a0.y, b0.y, acc[1], 0, 0, 0);
+  acc[2] = __builtin_amdgcn_mfma_f32_32x32x1f32(a0.z, b0.z, acc[2], 0, 0, 0);
+  acc[3] = __builtin_amdgcn_mfma_f32_32x32x1f32(a0.w, b0.w, acc[3], 0, 0, 0);
+  acc[4] = __builtin_amdgcn_mfma_f32_32x32x1f32(a1.x, b1.x, acc[4], 0, 0, 0);
+  acc[5] = __builtin_amdgcn_mfma_f32_32x32x1f32(a1.y, b1.y, acc[5], 0, 0, 0);
+  acc[6] = __builtin_amdgcn_mfma_f32_32x32x1f32(a1.z, b1.z, acc[6], 0, 0, 0);
+  acc[7] = __builtin_amdgcn_mfma_f32_32x32x1f32(a1.w, b1.w, acc[7], 0, 0, 0);
+}
+
 template <int LX, int LW>
 __global__ void __launch_bounds__(256) dot_mfma_k(MfmaOperand X, MfmaOperand W, int64_t N, int64_t M, int64_t K,
                                                   int tail, int tiles_m, float *__restrict__ Y) {
-  __shared__ float lds[2][2][kMT * kLS];  // [buffer][operand: 0 = lhs rows n, 1 = rhs rows m]
+  extern __shared__ float lds_m[];  // [buffer][operand: 0 = lhs rows n, 1 = rhs rows m][kMT * kLS]
+  auto tile = [&](int buf, int op) { return lds_m + (buf * 2 + op) * (kMT * kLS); };
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int wn = wave >> 1, wm = wave & 1;
   const int64_t b = blockIdx.y;
@@ -216,39 +237,29 @@ __global__ void __launch_bounds__(256) dot_mfma_k(MfmaOperand X, MfmaOperand W, 
 #pragma unroll
     for (int r = 0; r < 32; r++) acc[q][r] = 0.0f;
 
-  float4 rx[4], rw[4];
+  float4 rx[kRegs], rw[kRegs];
   if (nst > 0) {
     mfma_fetch<LX>(X, b, n0, 0, nb, rx);
     mfma_fetch<LW>(W, b, m0, 0, nb, rw);
-    mfma_stash<LX>(lds[0][0], rx);
-    mfma_stash<LW>(lds[0][1], rw);
+    mfma_stash<LX>(tile(0, 0), rx);
+    mfma_stash<LW>(tile(0, 1), rw);
   }
   __syncthreads();
   const int h = lane >> 5, li = lane & 31;
   for (int s = 0; s < nst; s++) {
     const int buf = s & 1;
-    if (s + 1 < nst) {
+    if (s + 1 < nst) {  // the next stage's loads fly while this stage's blocks run
       mfma_fetch<LX>(X, b, n0, s + 1, nb, rx);
       mfma_fetch<LW>(W, b, m0, s + 1, nb, rw);
     }
-    const float *xs = lds[buf][0] + (wn * 32 + li) * kLS + 8 * h;
-    const float *ws = lds[buf][1] + (wm * 32 + li) * kLS + 8 * h;
+    const float *xs = tile(buf, 0) + (wn * 32 + li) * kLS + 8 * h;
+    const float *ws = tile(buf, 1) + (wm * 32 + li) * kLS + 8 * h;
     const int blocks = min(kKC / 16, nb - s * (kKC / 16));
-    for (int blk = 0; blk < blocks; blk++) {
-      const float4 a0 = ld4(xs + 16 * blk), a1 = ld4(xs + 16 * blk + 4);
-      const float4 b0 = ld4(ws + 16 * blk), b1 = ld4(ws + 16 * blk + 4);
-      acc[0] = __builtin_amdgcn_mfma_f32_32x32x1f32(a0.x, b0.x, acc[0], 0, 0, 0);
-      acc[1] = __builtin_amdgcn_mfma_f32_32x32x1f32(a0.y, b0.y, acc[1], 0, 0, 0);
-      acc[2] = __builtin_amdgcn_mfma_f32_32x32x1f32(a0.z, b0.z, acc[2], 0, 0, 0);
-      acc[3] = __builtin_amdgcn_mfma_f32_32x32x1f32(a0.w, b0.w, acc[3], 0, 0, 0);
-      acc[4] = __builtin_amdgcn_mfma_f32_32x32x1f32(a1.x, b1.x, acc[4], 0, 0, 0);
-      acc[5] = __builtin_amdgcn_mfma_f32_32x32x1f32(a1.y, b1.y, acc[5], 0, 0, 0);
-      acc[6] = __builtin_amdgcn_mfma_f32_32x32x1f32(a1.z, b1.z, acc[6], 0, 0, 0);
-      acc[7] = __builtin_amdgcn_mfma_f32_32x32x1f32(a1.w, b1.w, acc[7], 0, 0, 0);
-    }
+    for (int blk = 0; blk < blocks; blk++)
+      mfma_block(acc, ld4(xs + 16 * blk), ld4(xs + 16 * blk + 4), ld4(ws + 16 * blk), ld4(ws + 16 * blk + 4));
     if (s + 1 < nst) {
-      mfma_stash<LX>(lds[buf ^ 1][0], rx);
-      mfma_stash<LW>(lds[buf ^ 1][1], rw);
+      mfma_stash<LX>(tile(buf ^ 1, 0), rx);
+      mfma_stash<LW>(tile(buf ^ 1, 1), rw);
     }
     __syncthreads();
   }
@@ -287,6 +298,8 @@ __global__ void __launch_bounds__(256) dot_mfma_k(MfmaOperand X, MfmaOperand W, 
     }
   }
 }
+
+constexpr int kDotLds = 2 * 2 * kMT * kLS * (int)sizeof(float);  // 135,168 bytes
 
 // ---- soft_max ---------------------------------------------------------------------
 
@@ -886,10 +899,21 @@ ArrayP dot_ggml(const DotOperand &lhs, const DotOperand &rhs, int64_t B, int64_t
     auto loader = [&](const float *p, int64_t sb, int64_t sf, int64_t sk, int64_t rows) {
       const bool al = ((uintptr_t)p % 16) == 0 && (sb % 4 == 0 || B == 1);
       if (al && sk == 1 && (sf % 4 == 0 || rows == 1)) return (int)kLoadRowVec;
-      if (al && sf == 1 && sk % 4 == 0 && rows % 4 == 0) return (int)kLoadColVec;
+      if (sf == 1) return (int)kLoadColVec;
       return (int)kLoadScalar;
     };
     const int lx = loader(L, lb, ln, lk, N), lw = loader(R, rb, rm, rk, M);
+    static const bool lds_ok = [] {  // 135 KB of dynamic LDS, above the 64 KB default
+#define DOT_ATTR(a, c)                                                                                       \
+  SHLO_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(&dot_mfma_k<a, c>),                          \
+                               hipFuncAttributeMaxDynamicSharedMemorySize, kDotLds));
+      DOT_ATTR(kLoadRowVec, kLoadRowVec) DOT_ATTR(kLoadRowVec, kLoadColVec) DOT_ATTR(kLoadRowVec, kLoadScalar)
+      DOT_ATTR(kLoadColVec, kLoadRowVec) DOT_ATTR(kLoadColVec, kLoadColVec) DOT_ATTR(kLoadColVec, kLoadScalar)
+      DOT_ATTR(kLoadScalar, kLoadRowVec) DOT_ATTR(kLoadScalar, kLoadColVec) DOT_ATTR(kLoadScalar, kLoadScalar)
+#undef DOT_ATTR
+      return true;
+    }();
+    (void)lds_ok;
     const MfmaOperand X{L, lb, ln, lk, N}, W{R, rb, rm, rk, M};
     const int tiles_m = (int)((M + kMT - 1) / kMT);
     const int64_t tiles = ((N + kMT - 1) / kMT) * tiles_m;
@@ -900,7 +924,7 @@ ArrayP dot_ggml(const DotOperand &lhs, const DotOperand &rhs, int64_t B, int64_t
       (void)kl, (void)kr;
 #define DOT_CASE(a, c)                                                                    \
   if (lx == a && lw == c) {                                                               \
-    dot_mfma_k<a, c><<<grid, 256, 0, s>>>(X, W, N, M, K, tl, tiles_m, Y);                \
+    dot_mfma_k<a, c><<<grid, 256, kDotLds, s>>>(X, W, N, M, K, tl, tiles_m, Y);          \
     return;                                                                               \
   }
       DOT_CASE(kLoadRowVec, kLoadRowVec) DOT_CASE(kLoadRowVec, kLoadColVec) DOT_CASE(kLoadRowVec, kLoadScalar)
