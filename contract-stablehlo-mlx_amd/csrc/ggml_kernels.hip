@@ -137,13 +137,17 @@ constexpr int kMT = 64;        // tile rows (n) and columns (m)
 constexpr int kKC = 128;       // k per stage (8 blocks of 16)
 constexpr int kLS = kKC + 4;   // LDS row stride (floats): rows start 4 banks apart
 constexpr int kRegs = kMT * kKC / 4 / 256;  // float4 per thread per operand per stage
+static_assert(kRegs % 4 == 0 && kMT == 64 && kKC % 64 == 0, "the loaders' thread mappings assume these");
 
 // How an operand tile is loaded: kLoadRowVec = rows contiguous in k (sk == 1),
 // float4 along k; kLoadColVec = free dim contiguous (sf == 1), four scalar
 // loads per thread (four consecutive k of one row, each load coalesced across
-// the wave along the free dim); kLoadScalar = any strides.  Every thread then
-// writes 16-byte [row][k] chunks to LDS.
-enum { kLoadRowVec = 0, kLoadColVec = 1, kLoadScalar = 2 };
+// the wave along the free dim); kLoadColQuad = the same operand 16-byte
+// aligned with rows % 4 == 0: each thread loads 4x4 (k x row) sub-blocks as
+// four 16-byte loads along the free dim and transposes them in registers;
+// kLoadScalar = any strides.  Every thread then writes 16-byte [row][k]
+// chunks to LDS.
+enum { kLoadRowVec = 0, kLoadColVec = 1, kLoadScalar = 2, kLoadColQuad = 3 };
 
 struct MfmaOperand {
   const float *p;
@@ -152,10 +156,40 @@ struct MfmaOperand {
 };
 
 // Stage s of one operand into registers: kMT * kKC floats per tile.
+// kLoadColQuad: sub-block u = t + 256 * (i / 4) of the tile's 16 x 32
+// (row quads x k quads); lane l of wave chunk c takes row quad l / 4 and k quad
+// l % 4 + 4 c, so the 16 lanes an LDS write serves together hit 16 distinct
+// bank quads, and each load reads four 256-byte runs along the free dim.
+// reg[4 (i / 4) + mm] ends up holding k quad kq of row 4 rq + mm.
+__device__ __forceinline__ void colquad_coords(int u, int &rq, int &kq) {
+  const int l = u % 64, c = u / 64;
+  rq = l / 4;
+  kq = l % 4 + 4 * c;
+}
+
 template <int LOAD>
 __device__ __forceinline__ void mfma_fetch(const MfmaOperand &o, int64_t b, int64_t r0, int s, int nb,
                                            float4 (&reg)[kRegs]) {
   const int t = threadIdx.x;
+  if (LOAD == kLoadColQuad) {
+#pragma unroll
+    for (int i = 0; i < kRegs / 4; i++) {
+      int rq, kq;
+      colquad_coords(t + 256 * i, rq, kq);
+      const int k = s * kKC + 4 * kq;
+      int64_t row = r0 + 4 * rq;
+      if (row > o.rows - 4) row = o.rows - 4;  // stays in bounds (rows % 4 == 0); discarded outputs
+      if (k / 16 < nb) {
+        const float *q = o.p + b * o.sb + row + (int64_t)k * o.sk;
+        const float4 v0 = ld4(q), v1 = ld4(q + o.sk), v2 = ld4(q + 2 * o.sk), v3 = ld4(q + 3 * o.sk);
+        reg[4 * i + 0] = make_float4(v0.x, v1.x, v2.x, v3.x);
+        reg[4 * i + 1] = make_float4(v0.y, v1.y, v2.y, v3.y);
+        reg[4 * i + 2] = make_float4(v0.z, v1.z, v2.z, v3.z);
+        reg[4 * i + 3] = make_float4(v0.w, v1.w, v2.w, v3.w);
+      }
+    }
+    return;
+  }
 #pragma unroll
   for (int i = 0; i < kRegs; i++) {
     const int f = t + 256 * i;
@@ -192,6 +226,16 @@ __device__ __forceinline__ void mfma_fetch(const MfmaOperand &o, int64_t b, int6
 template <int LOAD>
 __device__ __forceinline__ void mfma_stash(float *lds, const float4 (&reg)[kRegs]) {
   const int t = threadIdx.x;
+  if (LOAD == kLoadColQuad) {
+#pragma unroll
+    for (int i = 0; i < kRegs / 4; i++) {
+      int rq, kq;
+      colquad_coords(t + 256 * i, rq, kq);
+#pragma unroll
+      for (int mm = 0; mm < 4; mm++) st4(lds + (4 * rq + mm) * kLS + 4 * kq, reg[4 * i + mm]);
+    }
+    return;
+  }
 #pragma unroll
   for (int i = 0; i < kRegs; i++) {
     const int f = t + 256 * i;
@@ -899,6 +943,7 @@ ArrayP dot_ggml(const DotOperand &lhs, const DotOperand &rhs, int64_t B, int64_t
     auto loader = [&](const float *p, int64_t sb, int64_t sf, int64_t sk, int64_t rows) {
       const bool al = ((uintptr_t)p % 16) == 0 && (sb % 4 == 0 || B == 1);
       if (al && sk == 1 && (sf % 4 == 0 || rows == 1)) return (int)kLoadRowVec;
+      if (al && sf == 1 && sk % 4 == 0 && rows % 4 == 0) return (int)kLoadColQuad;
       if (sf == 1) return (int)kLoadColVec;
       return (int)kLoadScalar;
     };
@@ -910,6 +955,9 @@ ArrayP dot_ggml(const DotOperand &lhs, const DotOperand &rhs, int64_t B, int64_t
       DOT_ATTR(kLoadRowVec, kLoadRowVec) DOT_ATTR(kLoadRowVec, kLoadColVec) DOT_ATTR(kLoadRowVec, kLoadScalar)
       DOT_ATTR(kLoadColVec, kLoadRowVec) DOT_ATTR(kLoadColVec, kLoadColVec) DOT_ATTR(kLoadColVec, kLoadScalar)
       DOT_ATTR(kLoadScalar, kLoadRowVec) DOT_ATTR(kLoadScalar, kLoadColVec) DOT_ATTR(kLoadScalar, kLoadScalar)
+      DOT_ATTR(kLoadRowVec, kLoadColQuad) DOT_ATTR(kLoadColQuad, kLoadRowVec) DOT_ATTR(kLoadColQuad, kLoadColQuad)
+      DOT_ATTR(kLoadColQuad, kLoadColVec) DOT_ATTR(kLoadColVec, kLoadColQuad) DOT_ATTR(kLoadColQuad, kLoadScalar)
+      DOT_ATTR(kLoadScalar, kLoadColQuad)
 #undef DOT_ATTR
       return true;
     }();
@@ -930,6 +978,9 @@ ArrayP dot_ggml(const DotOperand &lhs, const DotOperand &rhs, int64_t B, int64_t
       DOT_CASE(kLoadRowVec, kLoadRowVec) DOT_CASE(kLoadRowVec, kLoadColVec) DOT_CASE(kLoadRowVec, kLoadScalar)
       DOT_CASE(kLoadColVec, kLoadRowVec) DOT_CASE(kLoadColVec, kLoadColVec) DOT_CASE(kLoadColVec, kLoadScalar)
       DOT_CASE(kLoadScalar, kLoadRowVec) DOT_CASE(kLoadScalar, kLoadColVec) DOT_CASE(kLoadScalar, kLoadScalar)
+      DOT_CASE(kLoadRowVec, kLoadColQuad) DOT_CASE(kLoadColQuad, kLoadRowVec) DOT_CASE(kLoadColQuad, kLoadColQuad)
+      DOT_CASE(kLoadColQuad, kLoadColVec) DOT_CASE(kLoadColVec, kLoadColQuad) DOT_CASE(kLoadColQuad, kLoadScalar)
+      DOT_CASE(kLoadScalar, kLoadColQuad)
 #undef DOT_CASE
     });
     return y;
