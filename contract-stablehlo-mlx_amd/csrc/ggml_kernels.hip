@@ -346,170 +346,227 @@ __global__ void __launch_bounds__(256) dot_mfma_k(MfmaOperand X, MfmaOperand W, 
 constexpr int kDotLds = 2 * 2 * kMT * kLS * (int)sizeof(float);  // 135,168 bytes
 
 // ---- soft_max ---------------------------------------------------------------------
+//
+// ggml_vec_soft_max_f32 adds each four-element group's part (a binary32
+// value >= 0) to a binary64 sum in group order, then the scalar tail values
+// (Shaders.lean:111-120).  That serial chain can be shortened wherever none of
+// its additions rounds.  Take a run of additions s + p_1 + ... + p_n (s the
+// running binary64 sum, p_i parts) and let u be the smallest ulp among s and
+// the nonzero p_i: a binary32 value is an integer multiple of its ulp
+// (2^(e-150) for exponent field e, 2^-149 for subnormals), a binary64 value
+// of its own.  If the exact total is below 2^53 u, every partial sum, in any
+// order, is a multiple of u below 2^53 u, hence a binary64 number: no addition
+// rounds, and the in-order chain, a tree sum and the exact total coincide.
+// The computed total t decides it: over at most 2^11 additions of
+// non-negative terms t falls short of the exact total by a relative 2^-42 at
+// most, so t <= (1 - 2^-20) 2^53 u implies an exact total below 2^53 u, and
+// then t is that total.
+//
+// softmax_inv first tests the whole row at once (a wave's tree sum T).  A row
+// that fails (parts spread over more than about 2^50, a NaN, an infinity)
+// still needs only inv = (float)(1.0 / S) of the in-order sum S, and
+// f(x) = (float)(1.0 / x) is non-increasing in x.  For n <= 2^11 non-negative
+// terms S lies within a relative (n-1) 2^-53 < 2^-42 of the exact total and T
+// within 2^-48 of it, so S lies in [T (1 - 2^-41), T (1 + 2^-41)], inside
+// [lo, hi] = T (1 -+ 2^-40) computed in binary64; f(lo) == f(hi) then fixes
+// f(S).  Only a row whose 1/S falls within about 2^-40 of a binary32 rounding
+// boundary fails that as well (about one row in 10^5 of those); it walks its
+// parts in segments of 16 consecutive groups (one 16-lane row of the wave,
+// reduced with DPP), adding a segment's tree sum in one step when the exactness
+// test holds for the running sum and that segment, and the segment's parts one
+// by one in group order when it does not.
 
-// The binary64 sum s = ((0 + p[0]) + p[1]) + ... + p[n-1] of n parts in LDS
-// (16-byte aligned), strictly in order.  The reads run one batch of 16 ahead
-// of the dependent adds, so the chain waits on the adds and not on the LDS.
-template <typename T>
-__device__ __forceinline__ double chain_sum_f64(const T *p, int n) {
-  constexpr int kB = 16;
-  constexpr int kV = 16 / (int)sizeof(T);  // elements per 16-byte read
-  using V = typename std::conditional<sizeof(T) == 4, float4, double2>::type;
-  double s = 0.0;
-  V cur[kB / kV], nxt[kB / kV];
-  const int nb = n / kB;
-  if (nb > 0) {
-#pragma unroll
-    for (int k = 0; k < kB / kV; k++) cur[k] = reinterpret_cast<const V *>(p)[k];
-  }
-#pragma unroll 1
-  for (int b = 0; b < nb; b++) {
-    // Unconditional (the last batch re-reads itself), so no branch makes the
-    // compiler wait for these reads before the adds below.
-    const T *q = p + (b + 1 < nb ? b + 1 : b) * kB;
-#pragma unroll
-    for (int k = 0; k < kB / kV; k++) nxt[k] = reinterpret_cast<const V *>(q)[k];
-#pragma unroll
-    for (int k = 0; k < kB / kV; k++) {
-      const T *e = reinterpret_cast<const T *>(&cur[k]);
-#pragma unroll
-      for (int m = 0; m < kV; m++) s = s + (double)e[m];
-    }
-#pragma unroll
-    for (int k = 0; k < kB / kV; k++) cur[k] = nxt[k];
-  }
-  for (int g = nb * kB; g < n; g++) s = s + (double)p[g];
-  return s;
+// Biased exponent e of p's ulp 2^(e-150) for a part p >= 0: its exponent
+// field, 1 for subnormals, 255 (no constraint) for +0.
+__device__ __forceinline__ int part_ulp_exp(float p) {
+  const uint32_t u = f_bits(p) & 0x7FFFFFFFu;
+  if (u == 0) return 255;
+  const int e = (int)(u >> 23);
+  return e > 1 ? e : 1;
 }
 
-// Doubles per row of parts in soft_max_rows_k: a multiple of 2 (16-byte rows
-// for the chain's double2 reads) with 2 spare, so the RB rows start in
-// different banks.
-__host__ __device__ inline int softmax_rows_part_stride(int G) { return (G + 1) / 2 * 2 + 2; }
+// (1 - 2^-20) 2^53 u for u = 2^(e-150), i.e. 2^(e-98) (2 - 2^-19): exponent
+// field e + 925, the top 19 fraction bits set.
+__device__ __forceinline__ double exact_limit(int e) {
+  return __builtin_bit_cast(double, ((uint64_t)(e + 925) << 52) | (((1ull << 19) - 1) << 33));
+}
 
-// ggml soft_max.  Lane l of a row's wave owns the four-element groups
-// g = l + 64j, loaded as float4 (coalesced).  The row maximum is a wave
-// reduction (exact: max is order-free on non-NaN data, and a +0/-0 tie
-// cannot change any output since exp(x - (+0)) = exp(x - (-0))); each group's
-// e = ggml_v_expf(x*sc - mx) stays in registers; each group's vaddvq_f32
-// part is added to a binary64 sum in group order (ggml_vec_soft_max_f32,
-// Shaders.lean:111-120); inv = (float)(1.0/sum), then y = e*inv.
-//
-// A block of 4*RPW rows: wave w loads rows w, w+4, ... (all loads first,
-// nontemporal: each byte is read once), then per row takes the wave max, keeps
-// the ggml_v_expf values in registers and writes each group's part to LDS as
-// binary64 (the conversion runs on every lane, off the serial path), one padded
-// row per row.  Then lane r of wave 0 runs row r's binary64 sum over the parts
-// in group order, so one v_add_f64 advances 4*RPW rows; the other waves wait
-// at the barrier.  Finally every wave scales and stores.
+// DPP within 16-lane rows: quad_perm [1,0,3,2], quad_perm [2,3,0,1],
+// row_half_mirror, row_mirror.  After the four steps every lane of a row holds
+// a reduction over the row's 16 lanes.
+constexpr int kDppXor1 = 0xB1, kDppXor2 = 0x4E, kDppHalfMirror = 0x141, kDppMirror = 0x140;
+template <int CTRL>
+__device__ __forceinline__ int dpp_i(int v) { return __builtin_amdgcn_mov_dpp(v, CTRL, 0xF, 0xF, true); }
+template <int CTRL>
+__device__ __forceinline__ double dpp_d(double v) {
+  const uint64_t u = __builtin_bit_cast(uint64_t, v);
+  const uint32_t lo = (uint32_t)dpp_i<CTRL>((int)(uint32_t)u), hi = (uint32_t)dpp_i<CTRL>((int)(uint32_t)(u >> 32));
+  return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
+}
+__device__ __forceinline__ double row16_sum(double v) {
+  v = v + dpp_d<kDppXor1>(v);
+  v = v + dpp_d<kDppXor2>(v);
+  v = v + dpp_d<kDppHalfMirror>(v);
+  return v + dpp_d<kDppMirror>(v);
+}
+__device__ __forceinline__ int row16_min(int v) {
+  v = min(v, dpp_i<kDppXor1>(v));
+  v = min(v, dpp_i<kDppXor2>(v));
+  v = min(v, dpp_i<kDppHalfMirror>(v));
+  return min(v, dpp_i<kDppMirror>(v));
+}
+__device__ __forceinline__ float lane_f(float v, int l) {
+  return bits_f((uint32_t)__builtin_amdgcn_readlane((int)f_bits(v), l));
+}
+__device__ __forceinline__ double lane_d(double v, int l) {
+  const uint64_t u = __builtin_bit_cast(uint64_t, v);
+  const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)u, l);
+  const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(u >> 32), l);
+  return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
+}
+
+// inv = (float)(1.0 / S) for the row whose group part g = l + 64 j lane l
+// holds as part[j] (+0 for g >= G), followed by tail values on lanes < T.
+// The result is the same on every lane.
+template <int J, bool FULL>
+__device__ __forceinline__ float softmax_inv(const float (&part)[J], int G, float tail, int T, int float_sum) {
+  const int lane = threadIdx.x % kWave;
+  if (float_sum) {  // planted: the denominator summed in binary32 (Shaders.lean:120-122)
+    float fs = 0.0f;
+#pragma unroll
+    for (int j = 0; j < J; j++) {
+      const int n = FULL ? kWave : min(kWave, G - kWave * j);
+      for (int l = 0; l < n; l++) fs = fs + lane_f(part[j], l);
+    }
+    for (int l = 0; l < T; l++) fs = fs + lane_f(tail, l);
+    return 1.0f / fs;
+  }
+  double ls = 0.0;
+  int le = 255;
+#pragma unroll
+  for (int j = 0; j < J; j++) {
+    ls = ls + (double)part[j];
+    le = min(le, part_ulp_exp(part[j]));
+  }
+  if (lane < T) {
+    ls = ls + (double)tail;
+    le = min(le, part_ulp_exp(tail));
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    ls = ls + __shfl_xor(ls, o, kWave);
+    le = min(le, __shfl_xor(le, o, kWave));
+  }
+  if (ls <= exact_limit(le)) return (float)(1.0 / ls);
+  const double d = ls * 0x1p-40;  // exact: ls >= 2^-149 or ls = 0
+  const float inv_lo = (float)(1.0 / (ls + d)), inv_hi = (float)(1.0 / (ls - d));
+  if (inv_lo == inv_hi) return inv_lo;  // false for NaN and infinity
+  // In order, segment by segment: segment q = 4 j + r holds groups
+  // 64 j + 16 r .. 64 j + 16 r + 15 (lanes 16 r .. 16 r + 15 of slice j).
+  double s = 0.0;
+#pragma unroll
+  for (int j = 0; j < J; j++) {
+    if (!FULL && kWave * j >= G) break;
+    const double seg = row16_sum((double)part[j]);
+    const int sege = row16_min(part_ulp_exp(part[j]));
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      if (!FULL && kWave * j + 16 * r >= G) break;
+      // u = min(ulp(s), the segment's smallest part ulp): the test splits
+      // into the segment's limit and s's own, (1 - 2^-20) 2^53 ulp(s), which
+      // is s's binade top 2^(E+1) less 2^-20 of it (no constraint for s = 0).
+      const double t = s + lane_d(seg, 16 * r);
+      const double lim_p = exact_limit(__builtin_amdgcn_readlane(sege, 16 * r));
+      const uint32_t hs = (uint32_t)(__builtin_bit_cast(uint64_t, s) >> 32);
+      const double lim_s = __builtin_bit_cast(double, (uint64_t)((hs & 0xFFF00000u) | 0x000FFFFEu) << 32);
+      if (t <= lim_p && (s == 0.0 || t <= lim_s)) {
+        s = t;
+      } else {
+        for (int i = 0; i < 16; i++) s = s + (double)lane_f(part[j], 16 * r + i);
+      }
+    }
+  }
+  for (int l = 0; l < T; l++) s = s + (double)lane_f(tail, l);
+  return (float)(1.0 / s);
+}
+
+// ggml soft_max, one wave per row.  Lane l owns the four-element groups
+// g = l + 64j, loaded as float4 (coalesced, nontemporal: each byte is read
+// once).  The row maximum is a wave reduction of v_max_f32: on rows without
+// NaN it equals ggml's (mx > w ? mx : w) chain in any order, and a +0/-0 tie
+// cannot change an output since exp(x - (+0)) = exp(x - (-0)); a NaN anywhere
+// in a row makes every output NaN through the sum, whatever the maximum.
+// Each group's e = ggml_v_expf(x*sc - mx) stays in registers, its
+// vaddvq_f32 part goes into softmax_inv, and y = e*inv.
 // FULL: every lane owns exactly J groups (cols == 256*J), so no group index
 // needs a bounds check.  UNIT: scale == 1, so x*sc is x (a NaN x makes the
 // whole row NaN either way, through its own part of the sum).
-//
-// The row maximum uses v_max_f32.  On rows without NaN it equals ggml's
-// (mx > w ? mx : w) chain in any order (a +0/-0 tie cannot change an
-// output); a NaN anywhere in a row makes every output NaN through the sum,
-// whatever the maximum.
-template <int J, int RPW, bool FULL, bool UNIT = false>
+template <int J, bool FULL, bool UNIT = false>
 __global__ void __launch_bounds__(256) soft_max_rows_k(int64_t rows, int cols, float sc, int float_sum,
                                                        const float *__restrict__ X, float *__restrict__ Y) {
-  extern __shared__ double lds_d[];
-  constexpr int RB = 4 * RPW;
   const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
   const int G = cols / 4;
-  const int PS = softmax_rows_part_stride(G);
-  double *parts = lds_d;
-  float *invs = reinterpret_cast<float *>(lds_d + RB * PS);
-  const int64_t row0 = blockIdx.x * (int64_t)RB;
-  float4 e[RPW][J];
+  const int64_t row = blockIdx.x * 4LL + wave;
+  if (row >= rows) return;  // the whole wave; no barrier follows
+  const float *x = X + row * cols;
+  float4 e[J];
 #pragma unroll
-  for (int rr = 0; rr < RPW; rr++) {
-    const int64_t row = row0 + wave + 4 * rr;
-    if (row >= rows) continue;
-    const float *x = X + row * cols;
+  for (int j = 0; j < J; j++) {
+    const int g = lane + kWave * j;
+    if (FULL || g < G) e[j] = ld4_nt(x + 4 * g);
+  }
+  float mx = -__builtin_inff();
 #pragma unroll
-    for (int j = 0; j < J; j++) {
-      const int g = lane + kWave * j;
-      if (FULL || g < G) e[rr][j] = ld4_nt(x + 4 * g);
+  for (int j = 0; j < J; j++) {
+    const int g = lane + kWave * j;
+    if (FULL || g < G) {
+      if (!UNIT) e[j] = make_float4(e[j].x * sc, e[j].y * sc, e[j].z * sc, e[j].w * sc);
+      mx = __builtin_fmaxf(mx, __builtin_fmaxf(__builtin_fmaxf(e[j].x, e[j].y), __builtin_fmaxf(e[j].z, e[j].w)));
     }
   }
 #pragma unroll
-  for (int rr = 0; rr < RPW; rr++) {
-    const int lr = wave + 4 * rr;
-    if (row0 + lr >= rows) continue;
-    float mx = -__builtin_inff();
+  for (int o = 32; o > 0; o >>= 1) mx = __builtin_fmaxf(mx, __shfl_xor(mx, o, kWave));
+  // The arguments x*sc - mx are <= 0 (or -inf, or NaN): the fast form, with
+  // the rare 126 < |n| <= 192 elements recomputed when any lane has one.
+  float4 v[J];
+  bool mid = false;
+#pragma unroll
+  for (int j = 0; j < J; j++) {
+    const int g = lane + kWave * j;
+    if (FULL || g < G) {
+      bool m0, m1, m2, m3;
+      v[j] = make_float4(e[j].x - mx, e[j].y - mx, e[j].z - mx, e[j].w - mx);  // e holds x*sc
+      e[j].x = ggml_v_expf_nonpos(v[j].x, &m0);
+      e[j].y = ggml_v_expf_nonpos(v[j].y, &m1);
+      e[j].z = ggml_v_expf_nonpos(v[j].z, &m2);
+      e[j].w = ggml_v_expf_nonpos(v[j].w, &m3);
+      mid |= m0 | m1 | m2 | m3;
+    }
+  }
+  if (__any(mid)) {
 #pragma unroll
     for (int j = 0; j < J; j++) {
       const int g = lane + kWave * j;
       if (FULL || g < G) {
-        if (!UNIT) e[rr][j] = make_float4(e[rr][j].x * sc, e[rr][j].y * sc, e[rr][j].z * sc, e[rr][j].w * sc);
-        mx = __builtin_fmaxf(mx, __builtin_fmaxf(__builtin_fmaxf(e[rr][j].x, e[rr][j].y),
-                                                 __builtin_fmaxf(e[rr][j].z, e[rr][j].w)));
+        e[j].x = ggml_v_expf(v[j].x);
+        e[j].y = ggml_v_expf(v[j].y);
+        e[j].z = ggml_v_expf(v[j].z);
+        e[j].w = ggml_v_expf(v[j].w);
       }
-    }
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) mx = __builtin_fmaxf(mx, __shfl_xor(mx, o, kWave));
-    // The arguments x*sc - mx are <= 0 (or -inf, or NaN): the fast form, with
-    // the rare 126 < |n| <= 192 elements recomputed when any lane has one.
-    float4 v[J];
-    bool mid = false;
-#pragma unroll
-    for (int j = 0; j < J; j++) {
-      const int g = lane + kWave * j;
-      if (FULL || g < G) {
-        bool m0, m1, m2, m3;
-        v[j] = make_float4(e[rr][j].x - mx, e[rr][j].y - mx, e[rr][j].z - mx, e[rr][j].w - mx);  // e holds x*sc
-        e[rr][j].x = ggml_v_expf_nonpos(v[j].x, &m0);
-        e[rr][j].y = ggml_v_expf_nonpos(v[j].y, &m1);
-        e[rr][j].z = ggml_v_expf_nonpos(v[j].z, &m2);
-        e[rr][j].w = ggml_v_expf_nonpos(v[j].w, &m3);
-        mid |= m0 | m1 | m2 | m3;
-      }
-    }
-    if (__any(mid)) {
-#pragma unroll
-      for (int j = 0; j < J; j++) {
-        const int g = lane + kWave * j;
-        if (FULL || g < G) {
-          e[rr][j].x = ggml_v_expf(v[j].x);
-          e[rr][j].y = ggml_v_expf(v[j].y);
-          e[rr][j].z = ggml_v_expf(v[j].z);
-          e[rr][j].w = ggml_v_expf(v[j].w);
-        }
-      }
-    }
-#pragma unroll
-    for (int j = 0; j < J; j++) {
-      const int g = lane + kWave * j;
-      if (FULL || g < G) parts[lr * PS + g] = (double)((e[rr][j].x + e[rr][j].y) + (e[rr][j].z + e[rr][j].w));
     }
   }
-  __syncthreads();
-  if (wave == 0 && lane < RB && row0 + lane < rows) {
-    const double *pr = parts + lane * PS;
-    float inv;
-    if (float_sum) {  // planted: the denominator summed in binary32 (Shaders.lean:120-122)
-      float fs = 0.0f;
-      for (int g = 0; g < G; g++) fs = fs + (float)pr[g];
-      inv = 1.0f / fs;
-    } else {
-      inv = (float)(1.0 / chain_sum_f64(pr, G));
-    }
-    invs[lane] = inv;
+  float part[J];
+#pragma unroll
+  for (int j = 0; j < J; j++) {
+    const int g = lane + kWave * j;
+    part[j] = (FULL || g < G) ? (e[j].x + e[j].y) + (e[j].z + e[j].w) : 0.0f;
   }
-  __syncthreads();
+  const float inv = softmax_inv<J, FULL>(part, G, 0.0f, 0, float_sum);
+  float *y = Y + row * cols;
 #pragma unroll
-  for (int rr = 0; rr < RPW; rr++) {
-    const int lr = wave + 4 * rr;
-    const int64_t row = row0 + lr;
-    if (row >= rows) continue;
-    const float inv = invs[lr];
-    float *y = Y + row * cols;
-#pragma unroll
-    for (int j = 0; j < J; j++) {
-      const int g = lane + kWave * j;
-      if (FULL || g < G) st4_nt(y + 4 * g, make_float4(e[rr][j].x * inv, e[rr][j].y * inv, e[rr][j].z * inv, e[rr][j].w * inv));
-    }
+  for (int j = 0; j < J; j++) {
+    const int g = lane + kWave * j;
+    if (FULL || g < G) st4_nt(y + 4 * g, make_float4(e[j].x * inv, e[j].y * inv, e[j].z * inv, e[j].w * inv));
   }
 }
 
@@ -518,17 +575,14 @@ __global__ void __launch_bounds__(256) soft_max_rows_k(int64_t rows, int cols, f
 // cols % 4 through the scalar expf, the correctly rounded one here, adding
 // each tail value to the binary64 sum after the group parts
 // (ggml_vec_soft_max_f32).  Rows are not 16-byte aligned, so elements are read
-// one by one; wave w of a block owns row 4*blockIdx.x + w and its lane 0 runs
-// the row's sum.
+// one by one; wave w of a block owns row 4*blockIdx.x + w.
 template <int J>
 __global__ void __launch_bounds__(256) soft_max_tail_k(int64_t rows, int cols, float sc, int float_sum,
                                                        const float *__restrict__ X, float *__restrict__ Y) {
-  extern __shared__ double lds_t[];
   const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
   const int G = cols / 4, T = cols % 4;
-  double *parts = lds_t + wave * softmax_rows_part_stride(G + T);
   const int64_t row = blockIdx.x * 4LL + wave;
-  if (row >= rows) return;  // the whole wave: no block barrier follows
+  if (row >= rows) return;  // the whole wave; no barrier follows
   const float *x = X + row * cols;
   float *y = Y + row * cols;
   float4 e[J];
@@ -556,33 +610,21 @@ __global__ void __launch_bounds__(256) soft_max_tail_k(int64_t rows, int cols, f
     const float other = __shfl_xor(mx, o, kWave);
     mx = mx > other ? mx : other;
   }
+  float part[J];
 #pragma unroll
   for (int j = 0; j < J; j++) {
     const int g = lane + kWave * j;
+    part[j] = 0.0f;
     if (g < G) {
       e[j].x = ggml_v_expf(e[j].x * sc - mx);
       e[j].y = ggml_v_expf(e[j].y * sc - mx);
       e[j].z = ggml_v_expf(e[j].z * sc - mx);
       e[j].w = ggml_v_expf(e[j].w * sc - mx);
-      parts[g] = (double)((e[j].x + e[j].y) + (e[j].z + e[j].w));
+      part[j] = (e[j].x + e[j].y) + (e[j].z + e[j].w);
     }
   }
-  if (lane < T) {
-    et = expfk::expf_cr(et * sc - mx);
-    parts[G + lane] = (double)et;
-  }
-  wave_sync();
-  float inv = 0.0f;
-  if (lane == 0) {
-    if (float_sum) {  // planted: the denominator summed in binary32 (Shaders.lean:120-122)
-      float fs = 0.0f;
-      for (int g = 0; g < G + T; g++) fs = fs + (float)parts[g];
-      inv = 1.0f / fs;
-    } else {
-      inv = (float)(1.0 / chain_sum_f64(parts, G + T));
-    }
-  }
-  inv = __shfl(inv, 0, kWave);
+  if (lane < T) et = expfk::expf_cr(et * sc - mx);
+  const float inv = softmax_inv<J, false>(part, G, et, T, float_sum);
 #pragma unroll
   for (int j = 0; j < J; j++) {
     const int g = lane + kWave * j;
@@ -596,122 +638,9 @@ __global__ void __launch_bounds__(256) soft_max_tail_k(int64_t rows, int cols, f
   if (lane < T) y[4 * G + lane] = et * inv;
 }
 
-// Doubles per row of parts in soft_max_pipe_k: even, so every row starts
-// 16-byte aligned for the double2 reads.
-__host__ __device__ inline int softmax_pipe_row_doubles(int G) { return (G + 1) / 2 * 2 + 2; }
-
-// Persistent, software-pipelined variant: each wave owns RPW rows at a time
-// (rows w*RPW .. w*RPW+RPW-1, then the same rows plus RPW*waves, ...).  While
-// the current rows are being exponentiated and summed, the next rows' loads are
-// already in flight.  Group parts are stored to the wave's own LDS region as
-// binary64 (converted by all lanes in parallel), and lane r runs row r's sum
-// in group order, so one v_add_f64 advances RPW rows and no block barrier is
-// needed.
-template <int J, int RPW>
-__global__ void __launch_bounds__(256) soft_max_pipe_k(int64_t rows, int cols, float sc, int float_sum,
-                                                       const float *__restrict__ X, float *__restrict__ Y) {
-  extern __shared__ double ldsd[];
-  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
-  const int G = cols / 4;
-  const int RS = softmax_pipe_row_doubles(G);
-  double *parts = ldsd + (size_t)wave * RPW * RS;
-  const int64_t gw = blockIdx.x * (int64_t)(blockDim.x / kWave) + wave;
-  const int64_t nw = (int64_t)gridDim.x * (blockDim.x / kWave);
-  float4 cur[RPW][J], nxt[RPW][J];
-  auto fetch = [&](int64_t r0, float4 (&dst)[RPW][J]) {
-#pragma unroll
-    for (int rr = 0; rr < RPW; rr++) {
-      const int64_t row = r0 + rr;
-      if (row >= rows) continue;
-      const float *x = X + row * cols;
-#pragma unroll
-      for (int j = 0; j < J; j++) {
-        const int g = lane + kWave * j;
-        if (g < G) dst[rr][j] = ld4(x + 4 * g);
-      }
-    }
-  };
-  int64_t r0 = gw * RPW;
-  if (r0 < rows) fetch(r0, cur);
-  for (; r0 < rows; r0 += nw * RPW) {
-    const int64_t n0 = r0 + nw * RPW;
-    if (n0 < rows) fetch(n0, nxt);
-#pragma unroll
-    for (int rr = 0; rr < RPW; rr++) {
-      if (r0 + rr >= rows) continue;
-      float mx = -__builtin_inff();
-#pragma unroll
-      for (int j = 0; j < J; j++) {
-        const int g = lane + kWave * j;
-        if (g < G) {
-          const float w0 = cur[rr][j].x * sc, w1 = cur[rr][j].y * sc, w2 = cur[rr][j].z * sc, w3 = cur[rr][j].w * sc;
-          mx = mx > w0 ? mx : w0;
-          mx = mx > w1 ? mx : w1;
-          mx = mx > w2 ? mx : w2;
-          mx = mx > w3 ? mx : w3;
-        }
-      }
-#pragma unroll
-      for (int o = 32; o > 0; o >>= 1) {
-        const float other = __shfl_xor(mx, o, kWave);
-        mx = mx > other ? mx : other;
-      }
-#pragma unroll
-      for (int j = 0; j < J; j++) {
-        const int g = lane + kWave * j;
-        if (g < G) {
-          cur[rr][j].x = ggml_v_expf(cur[rr][j].x * sc - mx);
-          cur[rr][j].y = ggml_v_expf(cur[rr][j].y * sc - mx);
-          cur[rr][j].z = ggml_v_expf(cur[rr][j].z * sc - mx);
-          cur[rr][j].w = ggml_v_expf(cur[rr][j].w * sc - mx);
-          const float part = (cur[rr][j].x + cur[rr][j].y) + (cur[rr][j].z + cur[rr][j].w);
-          if (float_sum) reinterpret_cast<float *>(parts + rr * RS)[g] = part;
-          else parts[rr * RS + g] = (double)part;
-        }
-      }
-    }
-    wave_sync();
-    float inv = 0.0f;
-    if (lane < RPW && r0 + lane < rows) {
-      if (float_sum) {  // planted: the denominator summed in binary32 (Shaders.lean:120-122)
-        const float *pr = reinterpret_cast<const float *>(parts + lane * RS);
-        float fs = 0.0f;
-        for (int g = 0; g < G; g++) fs = fs + pr[g];
-        inv = 1.0f / fs;
-      } else {
-        inv = (float)(1.0 / chain_sum_f64(parts + lane * RS, G));
-      }
-    }
-#pragma unroll
-    for (int rr = 0; rr < RPW; rr++) {
-      const float iv = __shfl(inv, rr, kWave);
-      const int64_t row = r0 + rr;
-      if (row >= rows) continue;
-      float *y = Y + row * cols;
-#pragma unroll
-      for (int j = 0; j < J; j++) {
-        const int g = lane + kWave * j;
-        if (g < G) st4(y + 4 * g, make_float4(cur[rr][j].x * iv, cur[rr][j].y * iv, cur[rr][j].z * iv, cur[rr][j].w * iv));
-      }
-    }
-    wave_sync();
-#pragma unroll
-    for (int rr = 0; rr < RPW; rr++)
-#pragma unroll
-      for (int j = 0; j < J; j++) cur[rr][j] = nxt[rr][j];
-  }
-}
-
 int env_int(const char *name, int dflt) {
   const char *s = getenv(name);
   return s ? atoi(s) : dflt;
-}
-
-int softmax_rows_per_wave(int J) {
-  static const int env = env_int("SHLO_SOFTMAX_RPW", 0);
-  if (J > 4) return 1;
-  if (env == 1 || env == 2 || env == 4) return env;
-  return 1;
 }
 
 // ---- norm ---------------------------------------------------------------------------
@@ -1034,9 +963,8 @@ ArrayP soft_max(const ArrayP &x0, int64_t rows, int64_t cols, uint32_t scale_bit
   if (rows == 0 || cols == 0) return y;
   const float sc = bits_f(scale_bits);
   if (cols % 4) {
-    const int G = (int)(cols / 4), T = (int)(cols % 4);
+    const int G = (int)(cols / 4);
     const int Jt = std::max(1, (G + kWave - 1) / kWave);
-    const int lds = 4 * softmax_rows_part_stride(G + T) * (int)sizeof(double);
     const int64_t nblk = (rows + 3) / 4;
     if (nblk > 0x7FFFFFFF) fail("ggml.soft_max: too many rows");
     const unsigned grid = (unsigned)nblk;
@@ -1048,7 +976,7 @@ ArrayP soft_max(const ArrayP &x0, int64_t rows, int64_t cols, uint32_t scale_bit
     launch([=](hipStream_t s) {
       (void)kx;
 #define SMT_CASE(n) \
-  case n: soft_max_tail_k<n><<<grid, 256, lds, s>>>(rows, c, sc, fs, px, py); break;
+  case n: soft_max_tail_k<n><<<grid, 256, 0, s>>>(rows, c, sc, fs, px, py); break;
       switch (Jt) {
         SMT_CASE(1) SMT_CASE(2) SMT_CASE(3) SMT_CASE(4) SMT_CASE(5) SMT_CASE(6) SMT_CASE(7) SMT_CASE(8)
         SMT_CASE(9) SMT_CASE(10) SMT_CASE(11) SMT_CASE(12) SMT_CASE(13) SMT_CASE(14) SMT_CASE(15) SMT_CASE(16)
@@ -1059,41 +987,12 @@ ArrayP soft_max(const ArrayP &x0, int64_t rows, int64_t cols, uint32_t scale_bit
     return y;
   }
   const int J = (int)((cols / 4 + kWave - 1) / kWave);
-  const int RPW = softmax_rows_per_wave(J);
   const float *px = (const float *)x->data();
   float *py = (float *)y->data();
   const int c = (int)cols;
   const int fs = float_sum ? 1 : 0;
   ArrayP kx = x;
-  static const int pipe_blocks = env_int("SHLO_SOFTMAX_PIPE", 0);
-  if (pipe_blocks > 0) {
-    const int64_t waves = (rows + RPW - 1) / RPW;
-    const unsigned grid = (unsigned)std::min<int64_t>((waves + 3) / 4, pipe_blocks);
-    const int lds = 4 * RPW * softmax_pipe_row_doubles((int)(cols / 4)) * (int)sizeof(double);
-    launch([=](hipStream_t s) {
-      (void)kx;
-#define SMP_CASE(n)                                                                                 \
-  case n:                                                                                           \
-    if (RPW == 4) soft_max_pipe_k<n, 4><<<grid, 256, lds, s>>>(rows, c, sc, fs, px, py);            \
-    else if (RPW == 2) soft_max_pipe_k<n, 2><<<grid, 256, lds, s>>>(rows, c, sc, fs, px, py);       \
-    else soft_max_pipe_k<n, 1><<<grid, 256, lds, s>>>(rows, c, sc, fs, px, py);                     \
-    break;
-#define SMP_CASE1(n) \
-  case n: soft_max_pipe_k<n, 1><<<grid, 256, lds, s>>>(rows, c, sc, fs, px, py); break;
-      switch (J) {
-        SMP_CASE(1) SMP_CASE(2) SMP_CASE(3) SMP_CASE(4) SMP_CASE1(5) SMP_CASE1(6) SMP_CASE1(7) SMP_CASE1(8)
-        SMP_CASE1(9) SMP_CASE1(10) SMP_CASE1(11) SMP_CASE1(12) SMP_CASE1(13) SMP_CASE1(14) SMP_CASE1(15)
-        SMP_CASE1(16)
-        default: break;
-      }
-#undef SMP_CASE
-#undef SMP_CASE1
-    });
-    return y;
-  }
-  const int PS = softmax_rows_part_stride((int)(cols / 4));
-  const int lds = 4 * RPW * PS * (int)sizeof(double) + 4 * RPW * (int)sizeof(float);
-  const int64_t nblk = (rows + 4 * RPW - 1) / (4 * RPW);
+  const int64_t nblk = (rows + 3) / 4;
   if (nblk > 0x7FFFFFFF) fail("ggml.soft_max: too many rows");
   const unsigned grid = (unsigned)nblk;
   const bool full = cols == 4LL * kWave * J;
@@ -1102,24 +1001,16 @@ ArrayP soft_max(const ArrayP &x0, int64_t rows, int64_t cols, uint32_t scale_bit
     (void)kx;
 #define SM_CASE(n)                                                                                  \
   case n:                                                                                           \
-    if (RPW == 4) soft_max_rows_k<n, 4, false><<<grid, 256, lds, s>>>(rows, c, sc, fs, px, py);     \
-    else if (RPW == 2) soft_max_rows_k<n, 2, false><<<grid, 256, lds, s>>>(rows, c, sc, fs, px, py);\
-    else if (full && unit) soft_max_rows_k<n, 1, true, true><<<grid, 256, lds, s>>>(rows, c, sc, fs, px, py); \
-    else if (full) soft_max_rows_k<n, 1, true><<<grid, 256, lds, s>>>(rows, c, sc, fs, px, py);     \
-    else soft_max_rows_k<n, 1, false><<<grid, 256, lds, s>>>(rows, c, sc, fs, px, py);              \
-    break;
-#define SM_CASE1(n)                                                                                 \
-  case n:                                                                                           \
-    if (full) soft_max_rows_k<n, 1, true><<<grid, 256, lds, s>>>(rows, c, sc, fs, px, py);          \
-    else soft_max_rows_k<n, 1, false><<<grid, 256, lds, s>>>(rows, c, sc, fs, px, py);              \
+    if (full && unit) soft_max_rows_k<n, true, true><<<grid, 256, 0, s>>>(rows, c, sc, fs, px, py); \
+    else if (full) soft_max_rows_k<n, true><<<grid, 256, 0, s>>>(rows, c, sc, fs, px, py);          \
+    else soft_max_rows_k<n, false><<<grid, 256, 0, s>>>(rows, c, sc, fs, px, py);                   \
     break;
     switch (J) {
-      SM_CASE(1) SM_CASE(2) SM_CASE(3) SM_CASE(4) SM_CASE1(5) SM_CASE1(6) SM_CASE1(7) SM_CASE1(8)
-      SM_CASE1(9) SM_CASE1(10) SM_CASE1(11) SM_CASE1(12) SM_CASE1(13) SM_CASE1(14) SM_CASE1(15) SM_CASE1(16)
+      SM_CASE(1) SM_CASE(2) SM_CASE(3) SM_CASE(4) SM_CASE(5) SM_CASE(6) SM_CASE(7) SM_CASE(8)
+      SM_CASE(9) SM_CASE(10) SM_CASE(11) SM_CASE(12) SM_CASE(13) SM_CASE(14) SM_CASE(15) SM_CASE(16)
       default: break;
     }
 #undef SM_CASE
-#undef SM_CASE1
   });
   return y;
 }

@@ -149,6 +149,105 @@ def test_softmax_subnormal_exps(oracle, cols):
     assert np.any((got > 0) & (got < np.float32(1.1754944e-38)))  # subnormal outputs reached
 
 
+def exact_sum_passes(x):
+    """Rows whose group parts pass the kernel's exactness test (tree sum
+    <= 2^52 u), estimated with numpy's expf: that decides which of the two
+    denominator paths a row takes."""
+    e = np.exp(x - x.max(1, keepdims=True)).astype(np.float32)
+    p = e.reshape(x.shape[0], -1, 4)
+    parts = ((p[..., 0] + p[..., 1]) + (p[..., 2] + p[..., 3])).astype(np.float32)
+    bits = parts.view(np.uint32)
+    le = np.where(bits == 0, 255, np.maximum(bits >> 23, 1)).min(1).astype(np.int64)
+    return parts.astype(np.float64).sum(1) <= np.ldexp(1.0, le - 98)
+
+
+@pytest.mark.parametrize("cols", [352, 1024, 4096])
+def test_softmax_denominator_paths(oracle, cols):
+    """Rows spread 4 to 48 below their maximum: the group parts' tree sum
+    (exact, so equal to the in-order binary64 sum) on some rows, the in-order
+    chain on the others; the planted binary32 denominator on both."""
+    import shlo_hip
+    rng = np.random.default_rng(100 + cols)
+    rows = 96
+    spread = np.linspace(4.0, 48.0, rows, dtype=np.float32)[:, None]
+    x = (-spread * rng.random((rows, cols), dtype=np.float32)).astype(np.float32)
+    x[:, 0] = 0.0
+    passes = exact_sum_passes(x)
+    assert 0.2 < passes.mean() < 0.8, passes.mean()
+    text = custom_call_module("ggml.soft_max", "scale = 0x3F800000 : f32", x.shape)
+    want = oracle.soft_max(x)
+    for compile in (True, False):
+        assert same_bits(run(text, [x], compile=compile)[0], want), compile
+    got = run(text, [x], faults=shlo_hip.fault_bits("soft_max_float_sum"))[0]
+    assert same_bits(got, oracle.soft_max(x, float_sum=True))
+
+
+def _find_logit(oracle, P):
+    """A logit a <= 0 with fl32(1 + ggml_v_expf(a)) == P, or None."""
+    P = np.float32(P)
+    a = np.float32(np.log(np.float64(P) - 1.0))
+    for _ in range(400):
+        v = np.float32(np.float32(1.0) + oracle.ggml_v_expf(a))
+        if v == P:
+            return a
+        a = np.nextafter(a, np.float32(np.inf) if v < P else np.float32(-np.inf), dtype=np.float32)
+    return None
+
+
+def _walk_rows(oracle, cols, count):
+    """Rows that fail both fast denominator tests, so the kernel walks their
+    parts in order: x = [0, a, -inf, -inf, body..., -70 x 4 (+ tail)] with the
+    first part P = fl32(1 + e(a)) chosen so that 1/S lies within 2^-40 of a
+    binary32 rounding boundary.  Half the rows have a body of -70 (tiny parts
+    the chain absorbs: S = P, every segment walked part by part), half a body
+    of logits whose parts m keep 15 segments exact (S = P + 254 m)."""
+    from test_softmax_exact_sum import kernel_inv, near_boundary
+    e = lambda v: oracle.ggml_v_expf(np.float32(v))
+    quad = lambda v: np.float32(np.float32(e(v) + e(v)) + np.float32(e(v) + e(v)))
+    G = cols // 4
+    v_m = np.float32(-15.25)
+    rows = []
+    for body in (np.float32(-70.0), v_m):
+        offset = 0.0 if body == -70.0 else float(G - 2) * float(quad(v_m))
+        found = 0
+        for P in near_boundary(offset, 200):
+            a = _find_logit(oracle, P)
+            if a is None:
+                continue
+            x = np.full(cols, body, np.float32)
+            x[0], x[1], x[2], x[3] = 0.0, a, -np.inf, -np.inf
+            x[4 * (G - 1):] = -70.0
+            parts = np.array([P] + [quad(body)] * (G - 2) + [quad(-70.0)], np.float32)
+            tail = [oracle.expf_cr(np.float32(-70.0))] * (cols % 4)
+            inv, path = kernel_inv(np.concatenate([parts, np.array(tail, np.float32)]))
+            assert path == "walk", (P, path)
+            rows.append(x)
+            found += 1
+            if found == count:
+                break
+        assert found == count
+    return np.stack(rows)
+
+
+@pytest.mark.parametrize("cols", [1024, 1023])
+def test_softmax_denominator_walk(oracle, cols):
+    """Rows whose denominator needs the in-order walk (see _walk_rows), next
+    to ordinary rows: bit for bit against the oracle.  cols = 1023 runs the
+    row-tail kernel (pinned flavour), whose three tail values follow the parts."""
+    import shlo_hip
+    walk = _walk_rows(oracle, cols, 6)
+    x, _ = oracle.fill_normal(21, 3.0, 20 * cols)
+    x = np.concatenate([walk, x.reshape(20, cols)]).astype(np.float32)
+    text = custom_call_module("ggml.soft_max", "scale = 0x3F800000 : f32", x.shape)
+    want = oracle.soft_max(x)
+    shlo_hip.set_flavor(1 if cols % 4 else 0)
+    try:
+        for compile in (True, False):
+            assert same_bits(run(text, [x], compile=compile)[0], want), compile
+    finally:
+        shlo_hip.set_flavor(0)
+
+
 @pytest.mark.parametrize("cols", [1, 2, 3, 5, 7, 13, 257, 1021, 4093, 4095])
 def test_softmax_row_tails_pinned(oracle, cols):
     """Rows with cols % 4 != 0 in the pinned flavour: the last cols % 4
