@@ -139,14 +139,53 @@ static_assert(kRegs % 4 == 0 && kMT == 64 && kKC % 64 == 0, "the loaders' thread
 // aligned with rows % 4 == 0: each thread loads 4x4 (k x row) sub-blocks as
 // four 16-byte loads along the free dim and transposes them in registers;
 // kLoadScalar = any strides.  Every thread then writes 16-byte [row][k]
-// chunks to LDS.
-enum { kLoadRowVec = 0, kLoadColVec = 1, kLoadScalar = 2, kLoadColQuad = 3 };
+// chunks to LDS.  kLoadRowVecB and kLoadColQuadB read the same elements as
+// kLoadRowVec and kLoadColQuad through buffer loads: one per-lane byte offset
+// fixed for the whole kernel, and every per-load and per-stage advance in the
+// scalar offset, so a stage's loads cost no vector ALU work and no branches.
+// They are chosen only when every read is in range by construction (rows a
+// multiple of 64, every stage full, offsets below 2^31).
+enum { kLoadRowVec = 0, kLoadColVec = 1, kLoadScalar = 2, kLoadColQuad = 3, kLoadRowVecB = 4, kLoadColQuadB = 5 };
+
+// The LDS layout a loader's stash writes: the buffer loaders share their
+// plain counterparts'.
+constexpr int stash_kind(int load) {
+  return load == kLoadRowVecB ? kLoadRowVec : load == kLoadColQuadB ? kLoadColQuad : load;
+}
 
 struct MfmaOperand {
   const float *p;
   int64_t sb, sf, sk;
   int64_t rows;  // N or M
 };
+
+// A buffer loader's per-workgroup state: the batch's buffer resource and the
+// lane's byte offset within it.
+struct BufOp {
+  __amdgpu_buffer_rsrc_t r;
+  int voff;
+};
+
+template <int LOAD>
+__device__ __forceinline__ BufOp buf_op(const MfmaOperand &o, int64_t b, int64_t r0) {
+  BufOp bo;
+  const int t = threadIdx.x;
+  bo.r = __builtin_amdgcn_make_buffer_rsrc((void *)(o.p + b * o.sb), (short)0, 0x7FFFFFFF, 0x00020000);
+  if (LOAD == kLoadRowVecB) {  // row t / 32, k quad t % 32 (as kLoadRowVec's load 0)
+    bo.voff = (int)(((r0 + t / 32) * o.sf + (t % 32) * 4) * 4);
+  } else if (LOAD == kLoadColQuadB) {  // row quad (t % 64) / 4, k 4 (t % 4) + 16 (t / 64) (as kLoadColQuad's group 0)
+    bo.voff = (int)((r0 + 4 * ((t % 64) / 4) + (4 * (t % 4) + 16 * (t / 64)) * o.sk) * 4);
+  } else {
+    bo.voff = 0;
+  }
+  return bo;
+}
+
+__device__ __forceinline__ float4 buf_ld4(const BufOp &bo, int soff) {
+  typedef float f4 __attribute__((ext_vector_type(4)));
+  const f4 v = __builtin_bit_cast(f4, __builtin_amdgcn_raw_buffer_load_b128(bo.r, bo.voff, soff, 0));
+  return make_float4(v.x, v.y, v.z, v.w);
+}
 
 // Stage s of one operand into registers: kMT * kKC floats per tile.
 // kLoadColQuad: sub-block u = t + 256 * (i / 4) of the tile's 16 x 32
@@ -160,31 +199,52 @@ __device__ __forceinline__ void colquad_coords(int u, int &rq, int &kq) {
   kq = l % 4 + 4 * c;
 }
 
-template <int LOAD>
-__device__ __forceinline__ void mfma_fetch(const MfmaOperand &o, int64_t b, int64_t r0, int s, int nb,
+// Registers [I0, I1) of stage s (all of it by default; the 4x4 loaders in
+// whole groups of 4).
+template <int LOAD, int I0 = 0, int I1 = kRegs>
+__device__ __forceinline__ void mfma_fetch(const MfmaOperand &o, const BufOp &bo, int64_t b, int64_t r0, int s, int nb,
                                            float4 (&reg)[kRegs]) {
+  static_assert((LOAD != kLoadColQuad && LOAD != kLoadColQuadB) || (I0 % 4 == 0 && I1 % 4 == 0), "whole groups");
   const int t = threadIdx.x;
+  if (LOAD == kLoadRowVecB) {  // load i: rows 8 i further, stage s: k 128 s further
+#pragma unroll
+    for (int i = I0; i < I1; i++) reg[i] = buf_ld4(bo, (int)((8 * i * o.sf + s * kKC) * 4));
+    return;
+  }
+  if (LOAD == kLoadColQuadB) {  // group g: k 64 g further, load mm: k mm further
+#pragma unroll
+    for (int g = I0 / 4; g < I1 / 4; g++) {
+      float4 v[4];
+#pragma unroll
+      for (int mm = 0; mm < 4; mm++) v[mm] = buf_ld4(bo, (int)((s * kKC + 64 * g + mm) * o.sk * 4));
+      reg[4 * g + 0] = make_float4(v[0].x, v[1].x, v[2].x, v[3].x);
+      reg[4 * g + 1] = make_float4(v[0].y, v[1].y, v[2].y, v[3].y);
+      reg[4 * g + 2] = make_float4(v[0].z, v[1].z, v[2].z, v[3].z);
+      reg[4 * g + 3] = make_float4(v[0].w, v[1].w, v[2].w, v[3].w);
+    }
+    return;
+  }
   if (LOAD == kLoadColQuad) {
 #pragma unroll
-    for (int i = 0; i < kRegs / 4; i++) {
+    for (int g = I0 / 4; g < I1 / 4; g++) {
       int rq, kq;
-      colquad_coords(t + 256 * i, rq, kq);
+      colquad_coords(t + 256 * g, rq, kq);
       const int k = s * kKC + 4 * kq;
       int64_t row = r0 + 4 * rq;
       if (row > o.rows - 4) row = o.rows - 4;  // stays in bounds (rows % 4 == 0); discarded outputs
       if (k / 16 < nb) {
         const float *q = o.p + b * o.sb + row + (int64_t)k * o.sk;
         const float4 v0 = ld4(q), v1 = ld4(q + o.sk), v2 = ld4(q + 2 * o.sk), v3 = ld4(q + 3 * o.sk);
-        reg[4 * i + 0] = make_float4(v0.x, v1.x, v2.x, v3.x);
-        reg[4 * i + 1] = make_float4(v0.y, v1.y, v2.y, v3.y);
-        reg[4 * i + 2] = make_float4(v0.z, v1.z, v2.z, v3.z);
-        reg[4 * i + 3] = make_float4(v0.w, v1.w, v2.w, v3.w);
+        reg[4 * g + 0] = make_float4(v0.x, v1.x, v2.x, v3.x);
+        reg[4 * g + 1] = make_float4(v0.y, v1.y, v2.y, v3.y);
+        reg[4 * g + 2] = make_float4(v0.z, v1.z, v2.z, v3.z);
+        reg[4 * g + 3] = make_float4(v0.w, v1.w, v2.w, v3.w);
       }
     }
     return;
   }
 #pragma unroll
-  for (int i = 0; i < kRegs; i++) {
+  for (int i = I0; i < I1; i++) {
     const int f = t + 256 * i;
     if (LOAD == kLoadColVec) {
       // Lane-consecutive rows (the contiguous free dim, so each of the four
@@ -216,30 +276,34 @@ __device__ __forceinline__ void mfma_fetch(const MfmaOperand &o, int64_t b, int6
   }
 }
 
-template <int LOAD>
+// Registers [I0, I1) of a stage (all of it by default) into LDS.
+template <int LOAD_, int I0 = 0, int I1 = kRegs>
 __device__ __forceinline__ void mfma_stash(float *lds, const float4 (&reg)[kRegs]) {
+  constexpr int LOAD = stash_kind(LOAD_);
   const int t = threadIdx.x;
-  if (LOAD == kLoadColQuad) {
 #pragma unroll
-    for (int i = 0; i < kRegs / 4; i++) {
+  for (int i = I0; i < I1; i++) {
+    if (LOAD == kLoadColQuad) {
       int rq, kq;
-      colquad_coords(t + 256 * i, rq, kq);
-#pragma unroll
-      for (int mm = 0; mm < 4; mm++) st4(lds + (4 * rq + mm) * kLS + 4 * kq, reg[4 * i + mm]);
-    }
-    return;
-  }
-#pragma unroll
-  for (int i = 0; i < kRegs; i++) {
-    const int f = t + 256 * i;
-    if (LOAD == kLoadColVec) {
+      colquad_coords(t + 256 * (i / 4), rq, kq);
+      st4(lds + (4 * rq + i % 4) * kLS + 4 * kq, reg[i]);
+    } else if (LOAD == kLoadColVec) {
+      const int f = t + 256 * i;
       const int row_l = f % kMT, kq = (f / kMT) * 4;
-      st4(lds + row_l * kLS + kq, reg[i]);  // rows 68 floats apart: 16 lanes, 16 distinct bank quads
+      st4(lds + row_l * kLS + kq, reg[i]);  // rows 132 floats apart: 16 lanes, 16 distinct bank quads
     } else {
+      const int f = t + 256 * i;
       const int row_l = f / (kKC / 4), kq = (f % (kKC / 4)) * 4;
       st4(lds + row_l * kLS + kq, reg[i]);
     }
   }
+}
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef const volatile __attribute__((address_space(3))) f32x4 lds_f32x4;
+__device__ __forceinline__ float4 ld4_lds_v(const float *p) {
+  const f32x4 v = *(lds_f32x4 *)(p);
+  return make_float4(v.x, v.y, v.z, v.w);
 }
 
 // One k-block of 16: the 8 fused multiply-adds per output, residues q and q+8.
@@ -275,9 +339,10 @@ __global__ void __launch_bounds__(256) dot_mfma_k(MfmaOperand X, MfmaOperand W, 
     for (int r = 0; r < 32; r++) acc[q][r] = 0.0f;
 
   float4 rx[kRegs], rw[kRegs];
+  const BufOp bx = buf_op<LX>(X, b, n0), bw = buf_op<LW>(W, b, m0);
   if (nst > 0) {
-    mfma_fetch<LX>(X, b, n0, 0, nb, rx);
-    mfma_fetch<LW>(W, b, m0, 0, nb, rw);
+    mfma_fetch<LX>(X, bx, b, n0, 0, nb, rx);
+    mfma_fetch<LW>(W, bw, b, m0, 0, nb, rw);
     mfma_stash<LX>(tile(0, 0), rx);
     mfma_stash<LW>(tile(0, 1), rw);
   }
@@ -285,18 +350,73 @@ __global__ void __launch_bounds__(256) dot_mfma_k(MfmaOperand X, MfmaOperand W, 
   const int h = lane >> 5, li = lane & 31;
   for (int s = 0; s < nst; s++) {
     const int buf = s & 1;
-    if (s + 1 < nst) {  // the next stage's loads fly while this stage's blocks run
-      mfma_fetch<LX>(X, b, n0, s + 1, nb, rx);
-      mfma_fetch<LW>(W, b, m0, s + 1, nb, rw);
-    }
     const float *xs = tile(buf, 0) + (wn * 32 + li) * kLS + 8 * h;
     const float *ws = tile(buf, 1) + (wm * 32 + li) * kLS + 8 * h;
     const int blocks = min(kKC / 16, nb - s * (kKC / 16));
-    for (int blk = 0; blk < blocks; blk++)
-      mfma_block(acc, ld4(xs + 16 * blk), ld4(xs + 16 * blk + 4), ld4(ws + 16 * blk), ld4(ws + 16 * blk + 4));
-    if (s + 1 < nst) {
-      mfma_stash<LX>(tile(buf ^ 1, 0), rx);
-      mfma_stash<LW>(tile(buf ^ 1, 1), rw);
+    // Software-pipelined with two operand sets in turn: block blk + 1's
+    // operands are read from LDS before block blk's matrix instructions issue
+    // (a read past the stage's last block re-reads it, so no read needs a
+    // branch).  The reads are volatile so that the compiler keeps them where
+    // they are written instead of sinking them next to their use, and a
+    // scheduling barrier keeps them ahead of the matrix instructions.
+    auto rd = [&](int k, float4 &x0, float4 &x1, float4 &w0, float4 &w1) {
+      const int o = 16 * (k < blocks ? k : blocks - 1);  // blocks >= 1 in every stage
+      x0 = ld4_lds_v(xs + o);
+      x1 = ld4_lds_v(xs + o + 4);
+      w0 = ld4_lds_v(ws + o);
+      w1 = ld4_lds_v(ws + o + 4);
+    };
+    // Straight-line code over the stage's kKC / 16 blocks (a loop header
+    // between blocks costs a full LDS wait); blocks past the end of a short
+    // last stage skip their matrix instructions.
+    float4 pa0, pa1, qa0, qa1, pb0, pb1, qb0, qb1;  // set p: even blocks, set q: odd blocks
+    rd(0, pa0, pa1, qa0, qa1);
+    // The next stage moves in four parts threaded between this stage's
+    // blocks: its loads after blocks 0..3 (a burst of 16 loads would hold up
+    // the matrix instructions queued behind them) and the matching LDS writes
+    // after blocks 4..7, four blocks after each part's loads (a short last
+    // stage has no next stage).
+    const bool more = s + 1 < nst;
+    auto part = [&](auto which) {
+      constexpr int q = decltype(which)::value;  // 0..3: loads, 4..7: LDS writes
+      constexpr int h = kRegs / 2;
+      if (more) {
+        if (q == 0) mfma_fetch<LX, 0, h>(X, bx, b, n0, s + 1, nb, rx);
+        if (q == 1) mfma_fetch<LX, h, kRegs>(X, bx, b, n0, s + 1, nb, rx);
+        if (q == 2) mfma_fetch<LW, 0, h>(W, bw, b, m0, s + 1, nb, rw);
+        if (q == 3) mfma_fetch<LW, h, kRegs>(W, bw, b, m0, s + 1, nb, rw);
+        if (q == 4) mfma_stash<LX, 0, h>(tile(buf ^ 1, 0), rx);
+        if (q == 5) mfma_stash<LX, h, kRegs>(tile(buf ^ 1, 0), rx);
+        if (q == 6) mfma_stash<LW, 0, h>(tile(buf ^ 1, 1), rw);
+        if (q == 7) mfma_stash<LW, h, kRegs>(tile(buf ^ 1, 1), rw);
+      }
+      __builtin_amdgcn_sched_barrier(0);
+    };
+    static_assert(kKC / 16 == 8 && kRegs % 8 == 0, "eight parts, one after each block");
+    using P0 = std::integral_constant<int, 0>;
+    using P1 = std::integral_constant<int, 1>;
+    using P2 = std::integral_constant<int, 2>;
+    using P3 = std::integral_constant<int, 3>;
+    using P4 = std::integral_constant<int, 4>;
+    using P5 = std::integral_constant<int, 5>;
+    using P6 = std::integral_constant<int, 6>;
+    using P7 = std::integral_constant<int, 7>;
+#pragma unroll
+    for (int blk = 0; blk < kKC / 16; blk += 2) {
+      rd(blk + 1, pb0, pb1, qb0, qb1);
+      __builtin_amdgcn_sched_barrier(0);
+      if (blk < blocks) mfma_block(acc, pa0, pa1, qa0, qa1);
+      if (blk == 0) part(P0());
+      if (blk == 2) part(P2());
+      if (blk == 4) part(P4());
+      if (blk == 6) part(P6());
+      if (blk + 2 < kKC / 16) rd(blk + 2, pa0, pa1, qa0, qa1);
+      __builtin_amdgcn_sched_barrier(0);
+      if (blk + 1 < blocks) mfma_block(acc, pb0, pb1, qb0, qb1);
+      if (blk == 0) part(P1());
+      if (blk == 2) part(P3());
+      if (blk == 4) part(P5());
+      if (blk == 6) part(P7());
     }
     __syncthreads();
   }
@@ -871,7 +991,21 @@ ArrayP dot_ggml(const DotOperand &lhs, const DotOperand &rhs, int64_t B, int64_t
       if (sf == 1) return (int)kLoadColVec;
       return (int)kLoadScalar;
     };
-    const int lx = loader(L, lb, ln, lk, N), lw = loader(R, rb, rm, rk, M);
+    int lx = loader(L, lb, ln, lk, N), lw = loader(R, rb, rm, rk, M);
+    // The buffer loaders need every read in range by construction: rows a
+    // multiple of the tile, every stage full, non-negative strides, and the
+    // largest byte offset within a batch below 2^31.
+    const bool full_stages = ((K / 16) % (kKC / 16)) == 0 && K >= kKC;
+    auto buf_ok = [&](int64_t sf, int64_t sk, int64_t sb, int64_t rows) {
+      if (rows % kMT || !full_stages || sf < 0 || sk < 0 || sb < 0) return false;
+      const int64_t top = ((rows - 1) * sf + (K - 1) * sk + 4) * 4;
+      return top < ((int64_t)1 << 31);
+    };
+    if (((lx == kLoadRowVec && ln % 4 == 0) || lx == kLoadColQuad) && buf_ok(ln, lk, lb, N) &&
+        ((lw == kLoadRowVec && rm % 4 == 0) || lw == kLoadColQuad) && buf_ok(rm, rk, rb, M)) {
+      lx = lx == kLoadRowVec ? (int)kLoadRowVecB : (int)kLoadColQuadB;
+      lw = lw == kLoadRowVec ? (int)kLoadRowVecB : (int)kLoadColQuadB;
+    }
     static const bool lds_ok = [] {  // 135 KB of dynamic LDS, above the 64 KB default
 #define DOT_ATTR(a, c)                                                                                       \
   SHLO_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(&dot_mfma_k<a, c>),                          \
@@ -882,6 +1016,8 @@ ArrayP dot_ggml(const DotOperand &lhs, const DotOperand &rhs, int64_t B, int64_t
       DOT_ATTR(kLoadRowVec, kLoadColQuad) DOT_ATTR(kLoadColQuad, kLoadRowVec) DOT_ATTR(kLoadColQuad, kLoadColQuad)
       DOT_ATTR(kLoadColQuad, kLoadColVec) DOT_ATTR(kLoadColVec, kLoadColQuad) DOT_ATTR(kLoadColQuad, kLoadScalar)
       DOT_ATTR(kLoadScalar, kLoadColQuad)
+      DOT_ATTR(kLoadRowVecB, kLoadRowVecB) DOT_ATTR(kLoadRowVecB, kLoadColQuadB)
+      DOT_ATTR(kLoadColQuadB, kLoadRowVecB) DOT_ATTR(kLoadColQuadB, kLoadColQuadB)
 #undef DOT_ATTR
       return true;
     }();
@@ -905,6 +1041,8 @@ ArrayP dot_ggml(const DotOperand &lhs, const DotOperand &rhs, int64_t B, int64_t
       DOT_CASE(kLoadRowVec, kLoadColQuad) DOT_CASE(kLoadColQuad, kLoadRowVec) DOT_CASE(kLoadColQuad, kLoadColQuad)
       DOT_CASE(kLoadColQuad, kLoadColVec) DOT_CASE(kLoadColVec, kLoadColQuad) DOT_CASE(kLoadColQuad, kLoadScalar)
       DOT_CASE(kLoadScalar, kLoadColQuad)
+      DOT_CASE(kLoadRowVecB, kLoadRowVecB) DOT_CASE(kLoadRowVecB, kLoadColQuadB)
+      DOT_CASE(kLoadColQuadB, kLoadRowVecB) DOT_CASE(kLoadColQuadB, kLoadColQuadB)
 #undef DOT_CASE
     });
     return y;
