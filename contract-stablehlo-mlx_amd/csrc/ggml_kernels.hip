@@ -114,23 +114,29 @@ __global__ void __launch_bounds__(256) dot_ggml_simple(int64_t n_out, int64_t N,
 // v_mfma_f32_32x32x1_2b_f32: per instruction every output of two 32x32 blocks
 // gets exactly one fused multiply-add, acc = fma(a_i, b_j, acc), with one
 // rounding (checked bit for bit against fmaf, subnormals included).  Block 0
-// of instruction q carries residue q, block 1 residue q + 8, so a wave holds
-// all 16 chains of its 32x32 outputs in 8 accumulator sets (256 registers).
+// of an instruction carries one residue and block 1 the residue 8 above it, so
+// the 16 chains of a 32x32 output tile take 8 accumulator sets (256 registers).
 // After the last block the fixed GGML_F32x4_REDUCE / vaddvq_f32 tree and the
 // serial tail run per output, exactly as in dot_finish.
 //
-// Workgroup: 4 waves on a 64 (n) x 64 (m) output tile; operands staged in LDS
-// as [row][k] (row stride KC + 4 floats), KC = 128 (eight k-blocks) per stage,
-// double-buffered (135 KB of gfx950's 160 KB), the next stage prefetched into
-// registers while the matrix cores work on the current one.
+// Workgroup: 8 waves (two per SIMD) on a 64 (n) x 64 (m) output tile, the two
+// waves of each 32x32 quadrant holding half of its chains each; operands staged
+// in LDS as [row][k] (row stride KC + 4 floats), KC = 128 (eight k-blocks) per
+// stage, double-buffered (135 KB of gfx950's 160 KB), the next stage loaded
+// into registers while the matrix cores work on the current one.
 
 typedef float v32f __attribute__((ext_vector_type(32)));
 
 constexpr int kMT = 64;        // tile rows (n) and columns (m)
 constexpr int kKC = 128;       // k per stage (8 blocks of 16)
 constexpr int kLS = kKC + 4;   // LDS row stride (floats): rows start 4 banks apart
-constexpr int kRegs = kMT * kKC / 4 / 256;  // float4 per thread per operand per stage
-static_assert(kRegs % 4 == 0 && kMT == 64 && kKC % 64 == 0, "the loaders' thread mappings assume these");
+// float4 per thread per operand per stage for a workgroup of TH threads.
+template <int TH>
+constexpr int regs_of() {
+  return kMT * kKC / 4 / TH;
+}
+static_assert(regs_of<512>() % 4 == 0 && kMT == 64 && kKC == 128,
+              "the loaders' thread mappings assume these");
 
 // How an operand tile is loaded: kLoadRowVec = rows contiguous in k (sk == 1),
 // float4 along k; kLoadColVec = free dim contiguous (sf == 1), four scalar
@@ -167,7 +173,7 @@ struct BufOp {
 };
 
 template <int LOAD>
-__device__ __forceinline__ BufOp buf_op(const MfmaOperand &o, int64_t b, int64_t r0) {
+__device__ __forceinline__ BufOp buf_op(const MfmaOperand &o, int64_t b, int64_t r0) {  // any TH <= 512
   BufOp bo;
   const int t = threadIdx.x;
   bo.r = __builtin_amdgcn_make_buffer_rsrc((void *)(o.p + b * o.sb), (short)0, 0x7FFFFFFF, 0x00020000);
@@ -188,7 +194,7 @@ __device__ __forceinline__ float4 buf_ld4(const BufOp &bo, int soff) {
 }
 
 // Stage s of one operand into registers: kMT * kKC floats per tile.
-// kLoadColQuad: sub-block u = t + 256 * (i / 4) of the tile's 16 x 32
+// kLoadColQuad: sub-block u = t + TH * (i / 4) of the tile's 16 x 32
 // (row quads x k quads); lane l of wave chunk c takes row quad l / 4 and k quad
 // l % 4 + 4 c, so the 16 lanes an LDS write serves together hit 16 distinct
 // bank quads, and each load reads four 256-byte runs along the free dim.
@@ -199,24 +205,24 @@ __device__ __forceinline__ void colquad_coords(int u, int &rq, int &kq) {
   kq = l % 4 + 4 * c;
 }
 
-// Registers [I0, I1) of stage s (all of it by default; the 4x4 loaders in
-// whole groups of 4).
-template <int LOAD, int I0 = 0, int I1 = kRegs>
+// Registers [I0, I1) of stage s for a workgroup of TH threads (all of it by
+// default; the 4x4 loaders in whole groups of 4).
+template <int LOAD, int TH, int I0 = 0, int I1 = regs_of<TH>()>
 __device__ __forceinline__ void mfma_fetch(const MfmaOperand &o, const BufOp &bo, int64_t b, int64_t r0, int s, int nb,
-                                           float4 (&reg)[kRegs]) {
+                                           float4 (&reg)[regs_of<TH>()]) {
   static_assert((LOAD != kLoadColQuad && LOAD != kLoadColQuadB) || (I0 % 4 == 0 && I1 % 4 == 0), "whole groups");
   const int t = threadIdx.x;
-  if (LOAD == kLoadRowVecB) {  // load i: rows 8 i further, stage s: k 128 s further
+  if (LOAD == kLoadRowVecB) {  // load i: rows TH / 32 * i further, stage s: k 128 s further
 #pragma unroll
-    for (int i = I0; i < I1; i++) reg[i] = buf_ld4(bo, (int)((8 * i * o.sf + s * kKC) * 4));
+    for (int i = I0; i < I1; i++) reg[i] = buf_ld4(bo, (int)(((TH / 32) * i * o.sf + s * kKC) * 4));
     return;
   }
-  if (LOAD == kLoadColQuadB) {  // group g: k 64 g further, load mm: k mm further
+  if (LOAD == kLoadColQuadB) {  // group g: k TH / 4 * g further, load mm: k mm further
 #pragma unroll
     for (int g = I0 / 4; g < I1 / 4; g++) {
       float4 v[4];
 #pragma unroll
-      for (int mm = 0; mm < 4; mm++) v[mm] = buf_ld4(bo, (int)((s * kKC + 64 * g + mm) * o.sk * 4));
+      for (int mm = 0; mm < 4; mm++) v[mm] = buf_ld4(bo, (int)((s * kKC + (TH / 4) * g + mm) * o.sk * 4));
       reg[4 * g + 0] = make_float4(v[0].x, v[1].x, v[2].x, v[3].x);
       reg[4 * g + 1] = make_float4(v[0].y, v[1].y, v[2].y, v[3].y);
       reg[4 * g + 2] = make_float4(v[0].z, v[1].z, v[2].z, v[3].z);
@@ -228,7 +234,7 @@ __device__ __forceinline__ void mfma_fetch(const MfmaOperand &o, const BufOp &bo
 #pragma unroll
     for (int g = I0 / 4; g < I1 / 4; g++) {
       int rq, kq;
-      colquad_coords(t + 256 * g, rq, kq);
+      colquad_coords(t + TH * g, rq, kq);
       const int k = s * kKC + 4 * kq;
       int64_t row = r0 + 4 * rq;
       if (row > o.rows - 4) row = o.rows - 4;  // stays in bounds (rows % 4 == 0); discarded outputs
@@ -245,7 +251,7 @@ __device__ __forceinline__ void mfma_fetch(const MfmaOperand &o, const BufOp &bo
   }
 #pragma unroll
   for (int i = I0; i < I1; i++) {
-    const int f = t + 256 * i;
+    const int f = t + TH * i;
     if (LOAD == kLoadColVec) {
       // Lane-consecutive rows (the contiguous free dim, so each of the four
       // loads is coalesced across the wave), four consecutive k per thread:
@@ -277,22 +283,22 @@ __device__ __forceinline__ void mfma_fetch(const MfmaOperand &o, const BufOp &bo
 }
 
 // Registers [I0, I1) of a stage (all of it by default) into LDS.
-template <int LOAD_, int I0 = 0, int I1 = kRegs>
-__device__ __forceinline__ void mfma_stash(float *lds, const float4 (&reg)[kRegs]) {
+template <int LOAD_, int TH, int I0 = 0, int I1 = regs_of<TH>()>
+__device__ __forceinline__ void mfma_stash(float *lds, const float4 (&reg)[regs_of<TH>()]) {
   constexpr int LOAD = stash_kind(LOAD_);
   const int t = threadIdx.x;
 #pragma unroll
   for (int i = I0; i < I1; i++) {
     if (LOAD == kLoadColQuad) {
       int rq, kq;
-      colquad_coords(t + 256 * (i / 4), rq, kq);
+      colquad_coords(t + TH * (i / 4), rq, kq);
       st4(lds + (4 * rq + i % 4) * kLS + 4 * kq, reg[i]);
     } else if (LOAD == kLoadColVec) {
-      const int f = t + 256 * i;
+      const int f = t + TH * i;
       const int row_l = f % kMT, kq = (f / kMT) * 4;
       st4(lds + row_l * kLS + kq, reg[i]);  // rows 132 floats apart: 16 lanes, 16 distinct bank quads
     } else {
-      const int f = t + 256 * i;
+      const int f = t + TH * i;
       const int row_l = f / (kKC / 4), kq = (f % (kKC / 4)) * 4;
       st4(lds + row_l * kLS + kq, reg[i]);
     }
@@ -306,130 +312,119 @@ __device__ __forceinline__ float4 ld4_lds_v(const float *p) {
   return make_float4(v.x, v.y, v.z, v.w);
 }
 
-// One k-block of 16: the 8 fused multiply-adds per output, residues q and q+8.
-__device__ __forceinline__ void mfma_block(v32f (&acc)[8], const float4 &a0, const float4 &a1, const float4 &b0,
-                                           const float4 &b1) {
-  acc[0] = __builtin_amdgcn_mfma_f32_32x32x1f32(a0.x, b0.x, acc[0], 0, 0, 0);
-  acc[1] = __builtin_amdgcn_mfma_f32_32x32x1f32(a0.y, b0.y, acc[1], 0, 0, 0);
-  acc[2] = __builtin_amdgcn_mfma_f32_32x32x1f32(a0.z, b0.z, acc[2], 0, 0, 0);
-  acc[3] = __builtin_amdgcn_mfma_f32_32x32x1f32(a0.w, b0.w, acc[3], 0, 0, 0);
-  acc[4] = __builtin_amdgcn_mfma_f32_32x32x1f32(a1.x, b1.x, acc[4], 0, 0, 0);
-  acc[5] = __builtin_amdgcn_mfma_f32_32x32x1f32(a1.y, b1.y, acc[5], 0, 0, 0);
-  acc[6] = __builtin_amdgcn_mfma_f32_32x32x1f32(a1.z, b1.z, acc[6], 0, 0, 0);
-  acc[7] = __builtin_amdgcn_mfma_f32_32x32x1f32(a1.w, b1.w, acc[7], 0, 0, 0);
+// Eight waves, two per SIMD, so that one wave's matrix instructions issue
+// while the other waits on memory, LDS or the barrier (with all 16 chains in
+// one wave, 256 accumulator registers leave room for one wave per SIMD, and
+// config 3 ran at 6.38 ms instead of 5.12).  The two waves of an output
+// quadrant split ggml's 16 chains: wave half rh
+// holds residues 4 rh .. 4 rh + 3 (block 0 of its four instructions) and
+// 4 rh + 8 .. 4 rh + 11 (block 1): 4 accumulator sets, 128 AGPRs.  Per block a
+// wave reads one float4 of each operand (k 16 b + 8 h + 4 rh ..) and issues 4
+// instructions.  In the epilogue the rh = 1 wave of each quadrant hands
+// a[4+q] + a[12+q] (q = 0..3, GGML_F32x4_REDUCE's sum[1] += sum[3]) through LDS
+// to the rh = 0 wave, which holds a[q] + a[8+q] (sum[0] += sum[2]) and finishes
+// the tree, the tail and the store.
+__device__ __forceinline__ void mfma_block4(v32f (&acc)[4], const float4 &a, const float4 &b) {
+  acc[0] = __builtin_amdgcn_mfma_f32_32x32x1f32(a.x, b.x, acc[0], 0, 0, 0);
+  acc[1] = __builtin_amdgcn_mfma_f32_32x32x1f32(a.y, b.y, acc[1], 0, 0, 0);
+  acc[2] = __builtin_amdgcn_mfma_f32_32x32x1f32(a.z, b.z, acc[2], 0, 0, 0);
+  acc[3] = __builtin_amdgcn_mfma_f32_32x32x1f32(a.w, b.w, acc[3], 0, 0, 0);
 }
 
 template <int LX, int LW>
-__global__ void __launch_bounds__(256) dot_mfma_k(MfmaOperand X, MfmaOperand W, int64_t N, int64_t M, int64_t K,
-                                                  int tail, int tiles_m, float *__restrict__ Y) {
-  extern __shared__ float lds_m[];  // [buffer][operand: 0 = lhs rows n, 1 = rhs rows m][kMT * kLS]
+__global__ void __launch_bounds__(512) dot_mfma8_k(MfmaOperand X, MfmaOperand W, int64_t N, int64_t M, int64_t K,
+                                                   int tail, int tiles_m, float *__restrict__ Y) {
+  constexpr int TH = 512, R = regs_of<TH>();
+  extern __shared__ float lds_m[];  // [buffer][operand][kMT * kLS]; the epilogue's exchange reuses it
   auto tile = [&](int buf, int op) { return lds_m + (buf * 2 + op) * (kMT * kLS); };
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int wn = wave >> 1, wm = wave & 1;
+  const int quad = wave & 3, rh = wave >> 2;
+  const int wn = quad >> 1, wm = quad & 1;
   const int64_t b = blockIdx.y;
   const int64_t n0 = (int64_t)(blockIdx.x / tiles_m) * kMT, m0 = (int64_t)(blockIdx.x % tiles_m) * kMT;
   const int64_t np = K & ~(int64_t)15;
   const int nb = (int)(np / 16);
   const int nst = (nb + kKC / 16 - 1) / (kKC / 16);
 
-  v32f acc[8];
+  v32f acc[4];
 #pragma unroll
-  for (int q = 0; q < 8; q++)
+  for (int q = 0; q < 4; q++)
 #pragma unroll
     for (int r = 0; r < 32; r++) acc[q][r] = 0.0f;
 
-  float4 rx[kRegs], rw[kRegs];
+  float4 rx[R], rw[R];
   const BufOp bx = buf_op<LX>(X, b, n0), bw = buf_op<LW>(W, b, m0);
   if (nst > 0) {
-    mfma_fetch<LX>(X, bx, b, n0, 0, nb, rx);
-    mfma_fetch<LW>(W, bw, b, m0, 0, nb, rw);
-    mfma_stash<LX>(tile(0, 0), rx);
-    mfma_stash<LW>(tile(0, 1), rw);
+    mfma_fetch<LX, TH>(X, bx, b, n0, 0, nb, rx);
+    mfma_fetch<LW, TH>(W, bw, b, m0, 0, nb, rw);
+    mfma_stash<LX, TH>(tile(0, 0), rx);
+    mfma_stash<LW, TH>(tile(0, 1), rw);
   }
   __syncthreads();
   const int h = lane >> 5, li = lane & 31;
   for (int s = 0; s < nst; s++) {
     const int buf = s & 1;
-    const float *xs = tile(buf, 0) + (wn * 32 + li) * kLS + 8 * h;
-    const float *ws = tile(buf, 1) + (wm * 32 + li) * kLS + 8 * h;
+    const float *xs = tile(buf, 0) + (wn * 32 + li) * kLS + 8 * h + 4 * rh;
+    const float *ws = tile(buf, 1) + (wm * 32 + li) * kLS + 8 * h + 4 * rh;
     const int blocks = min(kKC / 16, nb - s * (kKC / 16));
-    // Software-pipelined with two operand sets in turn: block blk + 1's
-    // operands are read from LDS before block blk's matrix instructions issue
-    // (a read past the stage's last block re-reads it, so no read needs a
-    // branch).  The reads are volatile so that the compiler keeps them where
-    // they are written instead of sinking them next to their use, and a
-    // scheduling barrier keeps them ahead of the matrix instructions.
-    auto rd = [&](int k, float4 &x0, float4 &x1, float4 &w0, float4 &w1) {
-      const int o = 16 * (k < blocks ? k : blocks - 1);  // blocks >= 1 in every stage
-      x0 = ld4_lds_v(xs + o);
-      x1 = ld4_lds_v(xs + o + 4);
-      w0 = ld4_lds_v(ws + o);
-      w1 = ld4_lds_v(ws + o + 4);
-    };
     // Straight-line code over the stage's kKC / 16 blocks (a loop header
     // between blocks costs a full LDS wait); blocks past the end of a short
-    // last stage skip their matrix instructions.
-    float4 pa0, pa1, qa0, qa1, pb0, pb1, qb0, qb1;  // set p: even blocks, set q: odd blocks
-    rd(0, pa0, pa1, qa0, qa1);
-    // The next stage moves in four parts threaded between this stage's
-    // blocks: its loads after blocks 0..3 (a burst of 16 loads would hold up
-    // the matrix instructions queued behind them) and the matching LDS writes
-    // after blocks 4..7, four blocks after each part's loads (a short last
-    // stage has no next stage).
+    // last stage skip their instructions.  Block blk + 1's operands are read
+    // before block blk's instructions issue: the reads are volatile so that
+    // the compiler keeps them where they are written instead of sinking them
+    // next to their use, and a scheduling barrier keeps them ahead of the
+    // instructions.  The next stage's loads follow blocks 0 and 1 (a burst of
+    // loads holds up the instructions queued behind it) and its LDS writes
+    // blocks 4 and 5, four blocks after the loads (a short last stage has no
+    // next stage).
+    auto rd = [&](int k, float4 &x, float4 &w) {
+      const int o = 16 * (k < blocks ? k : blocks - 1);  // blocks >= 1 in every stage
+      x = ld4_lds_v(xs + o);
+      w = ld4_lds_v(ws + o);
+    };
     const bool more = s + 1 < nst;
-    auto part = [&](auto which) {
-      constexpr int q = decltype(which)::value;  // 0..3: loads, 4..7: LDS writes
-      constexpr int h = kRegs / 2;
+    auto part = [&](int q) {
       if (more) {
-        if (q == 0) mfma_fetch<LX, 0, h>(X, bx, b, n0, s + 1, nb, rx);
-        if (q == 1) mfma_fetch<LX, h, kRegs>(X, bx, b, n0, s + 1, nb, rx);
-        if (q == 2) mfma_fetch<LW, 0, h>(W, bw, b, m0, s + 1, nb, rw);
-        if (q == 3) mfma_fetch<LW, h, kRegs>(W, bw, b, m0, s + 1, nb, rw);
-        if (q == 4) mfma_stash<LX, 0, h>(tile(buf ^ 1, 0), rx);
-        if (q == 5) mfma_stash<LX, h, kRegs>(tile(buf ^ 1, 0), rx);
-        if (q == 6) mfma_stash<LW, 0, h>(tile(buf ^ 1, 1), rw);
-        if (q == 7) mfma_stash<LW, h, kRegs>(tile(buf ^ 1, 1), rw);
+        if (q == 0) mfma_fetch<LX, TH>(X, bx, b, n0, s + 1, nb, rx);
+        if (q == 1) mfma_fetch<LW, TH>(W, bw, b, m0, s + 1, nb, rw);
+        if (q == 4) mfma_stash<LX, TH>(tile(buf ^ 1, 0), rx);
+        if (q == 5) mfma_stash<LW, TH>(tile(buf ^ 1, 1), rw);
       }
       __builtin_amdgcn_sched_barrier(0);
     };
-    static_assert(kKC / 16 == 8 && kRegs % 8 == 0, "eight parts, one after each block");
-    using P0 = std::integral_constant<int, 0>;
-    using P1 = std::integral_constant<int, 1>;
-    using P2 = std::integral_constant<int, 2>;
-    using P3 = std::integral_constant<int, 3>;
-    using P4 = std::integral_constant<int, 4>;
-    using P5 = std::integral_constant<int, 5>;
-    using P6 = std::integral_constant<int, 6>;
-    using P7 = std::integral_constant<int, 7>;
+    float4 pa, qa, pb, qb;  // set p: even blocks, set q: odd blocks
+    rd(0, pa, qa);
 #pragma unroll
     for (int blk = 0; blk < kKC / 16; blk += 2) {
-      rd(blk + 1, pb0, pb1, qb0, qb1);
+      rd(blk + 1, pb, qb);
       __builtin_amdgcn_sched_barrier(0);
-      if (blk < blocks) mfma_block(acc, pa0, pa1, qa0, qa1);
-      if (blk == 0) part(P0());
-      if (blk == 2) part(P2());
-      if (blk == 4) part(P4());
-      if (blk == 6) part(P6());
-      if (blk + 2 < kKC / 16) rd(blk + 2, pa0, pa1, qa0, qa1);
+      if (blk < blocks) mfma_block4(acc, pa, qa);
+      if (blk == 0 || blk == 4) part(blk);
+      if (blk + 2 < kKC / 16) rd(blk + 2, pa, qa);
       __builtin_amdgcn_sched_barrier(0);
-      if (blk + 1 < blocks) mfma_block(acc, pb0, pb1, qb0, qb1);
-      if (blk == 0) part(P1());
-      if (blk == 2) part(P3());
-      if (blk == 4) part(P5());
-      if (blk == 6) part(P7());
+      if (blk + 1 < blocks) mfma_block4(acc, pb, qb);
+      if (blk == 0 || blk == 4) part(blk + 1);
     }
     __syncthreads();
   }
 
-  // Epilogue: register r of set q holds block r/16 (residue q + 8*(r/16)) of
-  // output row i = 8*((r%16)/4) + 4*h + r%4, column j = lane%32.
+  // Epilogue: register r of set q holds block r/16 of output row
+  // i = 8*((r%16)/4) + 4*h + r%4, column j = lane%32.
+  float *xch = lds_m + quad * (16 * 4 * 64);  // [r][q][lane]
+  if (rh == 1) {
+#pragma unroll
+    for (int r = 0; r < 16; r++)
+#pragma unroll
+      for (int q = 0; q < 4; q++) xch[(r * 4 + q) * 64 + lane] = acc[q][r] + acc[q][r + 16];  // sum[1] += sum[3]
+  }
+  __syncthreads();
+  if (rh == 1) return;
 #pragma unroll
   for (int r = 0; r < 16; r++) {
-    float t8[8];
+    float w[4];
 #pragma unroll
-    for (int q = 0; q < 8; q++) t8[q] = acc[q][r] + acc[q][r + 16];   // sum[0]+=sum[2], sum[1]+=sum[3]
-    float u0 = t8[0] + t8[4], u1 = t8[1] + t8[5], u2 = t8[2] + t8[6], u3 = t8[3] + t8[7];  // sum[0]+=sum[1]
-    float sumf = (u0 + u1) + (u2 + u3);                                  // vaddvq_f32
+    for (int q = 0; q < 4; q++) w[q] = (acc[q][r] + acc[q][r + 16]) + xch[(r * 4 + q) * 64 + lane];  // sum[0]+=sum[2], +=sum[1]
+    float sumf = (w[0] + w[1]) + (w[2] + w[3]);                                                    // vaddvq_f32
     const int64_t n = n0 + wn * 32 + 8 * (r / 4) + 4 * h + (r % 4);
     const int64_t m = m0 + wm * 32 + li;
     if (n < N && m < M) {
@@ -457,6 +452,7 @@ __global__ void __launch_bounds__(256) dot_mfma_k(MfmaOperand X, MfmaOperand W, 
 }
 
 constexpr int kDotLds = 2 * 2 * kMT * kLS * (int)sizeof(float);  // 135,168 bytes
+static_assert(4 * 16 * 4 * 64 * (int)sizeof(float) <= kDotLds, "the epilogue exchange fits the stage buffers");
 
 // ---- soft_max ---------------------------------------------------------------------
 //
@@ -1008,7 +1004,7 @@ ArrayP dot_ggml(const DotOperand &lhs, const DotOperand &rhs, int64_t B, int64_t
     }
     static const bool lds_ok = [] {  // 135 KB of dynamic LDS, above the 64 KB default
 #define DOT_ATTR(a, c)                                                                                       \
-  SHLO_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(&dot_mfma_k<a, c>),                          \
+  SHLO_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(&dot_mfma8_k<a, c>),                         \
                                hipFuncAttributeMaxDynamicSharedMemorySize, kDotLds));
       DOT_ATTR(kLoadRowVec, kLoadRowVec) DOT_ATTR(kLoadRowVec, kLoadColVec) DOT_ATTR(kLoadRowVec, kLoadScalar)
       DOT_ATTR(kLoadColVec, kLoadRowVec) DOT_ATTR(kLoadColVec, kLoadColVec) DOT_ATTR(kLoadColVec, kLoadScalar)
@@ -1032,7 +1028,7 @@ ArrayP dot_ggml(const DotOperand &lhs, const DotOperand &rhs, int64_t B, int64_t
       (void)kl, (void)kr;
 #define DOT_CASE(a, c)                                                                    \
   if (lx == a && lw == c) {                                                               \
-    dot_mfma_k<a, c><<<grid, 256, kDotLds, s>>>(X, W, N, M, K, tl, tiles_m, Y);          \
+    dot_mfma8_k<a, c><<<grid, 512, kDotLds, s>>>(X, W, N, M, K, tl, tiles_m, Y);         \
     return;                                                                               \
   }
       DOT_CASE(kLoadRowVec, kLoadRowVec) DOT_CASE(kLoadRowVec, kLoadColVec) DOT_CASE(kLoadRowVec, kLoadScalar)
