@@ -158,6 +158,106 @@ __global__ void __launch_bounds__(kBlock) copy_nd(NDMap<2> map, uint32_t n, cons
   }
 }
 
+// ---- four elements per thread ---------------------------------------------------
+//
+// For 4-byte element types whose collapsed innermost dim has a length that is a
+// multiple of 4 and that every operand walks with stride 0 or 1: the map runs
+// over groups of four (innermost length / 4, innermost strides x 4), a stride-1
+// operand's group is one 16-byte access, a stride-0 operand's one scalar.
+// Results are the same elements computed by the same functor, so the bits
+// match the one-element kernels.
+
+template <class T>
+struct V4 {
+  T v[4];
+};
+
+template <class T>
+__device__ __forceinline__ V4<T> ld_v4(const T *p, bool unit) {
+  V4<T> r;
+  if (unit) {
+    const uint4 u = *reinterpret_cast<const uint4 *>(p);
+    r.v[0] = __builtin_bit_cast(T, u.x);
+    r.v[1] = __builtin_bit_cast(T, u.y);
+    r.v[2] = __builtin_bit_cast(T, u.z);
+    r.v[3] = __builtin_bit_cast(T, u.w);
+  } else {
+    r.v[0] = r.v[1] = r.v[2] = r.v[3] = *p;
+  }
+  return r;
+}
+
+template <class T>
+__device__ __forceinline__ void st_v4(T *p, const V4<T> &r) {
+  *reinterpret_cast<uint4 *>(p) = make_uint4(__builtin_bit_cast(uint32_t, r.v[0]), __builtin_bit_cast(uint32_t, r.v[1]),
+                                             __builtin_bit_cast(uint32_t, r.v[2]), __builtin_bit_cast(uint32_t, r.v[3]));
+}
+
+// unit[j]: operand j walks the innermost dim with stride 1 (else 0).
+template <class F, class TA, class TO>
+__global__ void __launch_bounds__(kBlock) ew1_v4(NDMap<1> map, uint32_t n4, const TA *a, TO *o, F f, bool ua) {
+  for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += gridDim.x * blockDim.x) {
+    uint32_t off[1];
+    map.offsets(i, off);
+    const V4<TA> x = ld_v4(a + off[0], ua);
+    V4<TO> y;
+#pragma unroll
+    for (int k = 0; k < 4; k++) y.v[k] = f(x.v[k]);
+    st_v4(o + 4 * (size_t)i, y);
+  }
+}
+
+template <class F, class TA, class TB, class TO>
+__global__ void __launch_bounds__(kBlock) ew2_v4(NDMap<2> map, uint32_t n4, const TA *a, const TB *b, TO *o, F f,
+                                                bool ua, bool ub) {
+  for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += gridDim.x * blockDim.x) {
+    uint32_t off[2];
+    map.offsets(i, off);
+    const V4<TA> x = ld_v4(a + off[0], ua);
+    const V4<TB> y = ld_v4(b + off[1], ub);
+    V4<TO> z;
+#pragma unroll
+    for (int k = 0; k < 4; k++) z.v[k] = f(x.v[k], y.v[k]);
+    st_v4(o + 4 * (size_t)i, z);
+  }
+}
+
+template <class T>
+__global__ void __launch_bounds__(kBlock) copy_v4(NDMap<2> map, uint32_t n4, const T *src, T *dst, bool us) {
+  for (uint32_t i = blockIdx.x * blockDim.x + threadIdx.x; i < n4; i += gridDim.x * blockDim.x) {
+    uint32_t off[2];
+    map.offsets(i, off);
+    st_v4(dst + off[1], ld_v4(src + off[0], us));
+  }
+}
+
+// The group map for `m` (element offsets in units of T), or false when the
+// four-element kernels do not apply: the innermost length is not a multiple
+// of 4, an operand walks it with a stride other than 0 or 1, or a stride-1
+// operand's groups would not be 16-byte aligned.  `ptrs[j]` is operand j's
+// base; `must_unit` marks operands (outputs) that need stride 1.
+template <int NOP>
+bool group_map(const NDMap<NOP> &m, const void *const (&ptrs)[NOP], const bool (&must_unit)[NOP], NDMap<NOP> &g,
+               bool (&unit)[NOP]) {
+  const int l = m.rank - 1;
+  if (m.dim[l] % 4) return false;
+  for (int j = 0; j < NOP; j++) {
+    const uint32_t sl = m.st[j][l];
+    if (sl > 1 || (must_unit[j] && sl != 1)) return false;
+    unit[j] = sl == 1;
+    if (unit[j]) {
+      if ((uintptr_t)ptrs[j] % 16) return false;
+      for (int d = 0; d < l; d++)
+        if (m.st[j][d] % 4) return false;
+    }
+  }
+  g = m;
+  g.dim[l] = m.dim[l] / 4;
+  g.div[l] = make_fastdiv(g.dim[l]);
+  for (int j = 0; j < NOP; j++) g.st[j][l] = m.st[j][l] * 4;
+  return true;
+}
+
 // ---- dtype dispatch -----------------------------------------------------------
 
 using f16 = _Float16;
@@ -334,6 +434,19 @@ void launch1(const ArrayP &a, const std::shared_ptr<Array> &o, F f) {
   const TA *pa = (const TA *)a->data();
   TO *po = (TO *)o->data();
   ArrayP keep = a;
+  if constexpr (sizeof(TA) == 4 && sizeof(TO) == 4) {
+    NDMap<1> g;
+    bool unit[1];
+    if ((uintptr_t)po % 16 == 0 && group_map<1>(m, {pa}, {false}, g, unit)) {
+      const uint32_t n4 = (uint32_t)(n / 4);
+      const bool ua = unit[0];
+      launch([=](hipStream_t s) {
+        (void)keep;
+        ew1_v4<F, TA, TO><<<grid_for(n4), kBlock, 0, s>>>(g, n4, pa, po, f, ua);
+      });
+      return;
+    }
+  }
   launch([=](hipStream_t s) {
     (void)keep;
     ew1<F, TA, TO><<<grid_for(n), kBlock, 0, s>>>(m, (uint32_t)n, pa, po, f);
@@ -361,6 +474,19 @@ void launch2(const ArrayP &a, const ArrayP &b, const std::shared_ptr<Array> &o, 
     }
   }
   auto m = make_map<2>(o->shape, {&a->strides, &b->strides});
+  if constexpr (sizeof(TA) == 4 && sizeof(TB) == 4 && sizeof(TO) == 4) {
+    NDMap<2> g;
+    bool unit[2];
+    if ((uintptr_t)po % 16 == 0 && group_map<2>(m, {pa, pb}, {false, false}, g, unit)) {
+      const uint32_t n4 = (uint32_t)(n / 4);
+      const bool ua = unit[0], ub = unit[1];
+      launch([=](hipStream_t s) {
+        (void)ka, (void)kb;
+        ew2_v4<F, TA, TB, TO><<<grid_for(n4), kBlock, 0, s>>>(g, n4, pa, pb, po, f, ua, ub);
+      });
+      return;
+    }
+  }
   launch([=](hipStream_t s) {
     (void)ka, (void)kb;
     ew2<F, TA, TB, TO><<<grid_for(n), kBlock, 0, s>>>(m, (uint32_t)n, pa, pb, po, f);
@@ -376,6 +502,19 @@ void launch_copy(const ArrayP &src, const Shape &dst_strides, char *dst_base, co
   const T *ps = (const T *)src->data();
   T *pd = (T *)dst_base;
   ArrayP keep = src;
+  if constexpr (sizeof(T) == 4) {
+    NDMap<2> g;
+    bool unit[2];
+    if (group_map<2>(m, {ps, pd}, {false, true}, g, unit)) {
+      const uint32_t n4 = (uint32_t)(n / 4);
+      const bool us = unit[0];
+      launch([=](hipStream_t s) {
+        (void)keep;
+        copy_v4<T><<<grid_for(n4), kBlock, 0, s>>>(g, n4, ps, pd, us);
+      });
+      return;
+    }
+  }
   launch([=](hipStream_t s) {
     (void)keep;
     copy_nd<T><<<grid_for(n), kBlock, 0, s>>>(m, (uint32_t)n, ps, pd);
