@@ -458,8 +458,203 @@ __global__ void __launch_bounds__(512) dot_mfma8_k(MfmaOperand X, MfmaOperand W,
   }
 }
 
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+typedef const volatile __attribute__((address_space(3))) f32x2 lds_f32x2;
+__device__ __forceinline__ float2 ld2_lds_v(const float *p) {
+  const f32x2 v = *(lds_f32x2 *)(p);
+  return make_float2(v.x, v.y);
+}
+
+// Persistent form: one workgroup per CU walks output tiles t = blockIdx.x,
+// blockIdx.x + gridDim.x, ..., and its stage pipeline runs straight across
+// tile boundaries, so the next tile's loads and LDS writes overlap this
+// tile's last stage and epilogue (a tile with K = 64 has one short stage).
+// The epilogue's exchange uses the stage buffer the tile's last stage read
+// from: the stage barrier ends its reads, the next tile's first stage went to
+// the other buffer, and the barrier after the epilogue keeps the next stage's
+// LDS writes out of it until the exchange has been read.  Tiles run
+// round-robin, so the workgroups that share an rhs tile at one time sit on one
+// XCD (for 4 row tiles per rhs tile).
+// PAIRS = false splits the chains as dot_mfma8_k does (one float4 of each
+// operand per block, four values per output exchanged).  PAIRS = true gives
+// the rh = 0 wave the residue pairs (r, r + 8) for r in {0, 1, 4, 5} and the
+// rh = 1 wave r in {2, 3, 6, 7}: each finishes w_r = (a[r] + a[r+8]) +
+// (a[r+4] + a[r+12]) for two r of GGML_F32x4_REDUCE and adds its pair,
+// (w0 + w1) or (w2 + w3), so one value per output crosses for vaddvq_f32's
+// (w0 + w1) + (w2 + w3); a block then takes two float2 of each operand
+// (k 16 b + 8 h + 2 rh and + 4).  The smaller exchange pays where the
+// epilogue is a large share of a tile (short K); the float4 reads where it is
+// not.
+template <int LX, int LW, bool PAIRS>
+__global__ void __launch_bounds__(512) dot_mfma8p_k(MfmaOperand X, MfmaOperand W, int64_t N, int64_t M, int64_t K,
+                                                    int tail, int tiles_m, int64_t tiles_b, int64_t tiles,
+                                                    float *__restrict__ Y) {
+  constexpr int TH = 512, R = regs_of<TH>();
+  extern __shared__ float lds_m[];  // [buffer][operand][kMT * kLS]
+  auto tile = [&](int buf, int op) { return lds_m + (buf * 2 + op) * (kMT * kLS); };
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int quad = wave & 3, rh = wave >> 2;
+  const int wn = quad >> 1, wm = quad & 1;
+  const int h = lane >> 5, li = lane & 31;
+  const int64_t np = K & ~(int64_t)15;
+  const int nb = (int)(np / 16);
+  const int nst = (nb + kKC / 16 - 1) / (kKC / 16);
+  int64_t t = blockIdx.x;  // the host launches at most `tiles` workgroups
+  auto tile_b = [&](int64_t tt) { return tt / tiles_b; };
+  auto tile_n0 = [&](int64_t tt) { return ((tt % tiles_b) / tiles_m) * kMT; };
+  auto tile_m0 = [&](int64_t tt) { return ((tt % tiles_b) % tiles_m) * kMT; };
+  int64_t b = tile_b(t), n0 = tile_n0(t), m0 = tile_m0(t);
+  BufOp bx = buf_op<LX>(X, b, n0), bw = buf_op<LW>(W, b, m0);
+
+  float4 rx[R], rw[R];
+  if (nst > 0) {
+    mfma_fetch<LX, TH>(X, bx, b, n0, 0, nb, rx);
+    mfma_fetch<LW, TH>(W, bw, b, m0, 0, nb, rw);
+    mfma_stash<LX, TH>(tile(0, 0), rx);
+    mfma_stash<LW, TH>(tile(0, 1), rw);
+  }
+  __syncthreads();
+  int buf = 0;
+  v32f acc[4];
+  for (;;) {
+#pragma unroll
+    for (int q = 0; q < 4; q++)
+#pragma unroll
+      for (int r = 0; r < 32; r++) acc[q][r] = 0.0f;
+    const int64_t tn = t + gridDim.x;
+    const bool has_next = tn < tiles;
+    const int64_t nb_ = has_next ? tile_b(tn) : b, nn0 = has_next ? tile_n0(tn) : n0,
+                  nm0 = has_next ? tile_m0(tn) : m0;
+    const BufOp nbx = buf_op<LX>(X, nb_, nn0), nbw = buf_op<LW>(W, nb_, nm0);
+    for (int s = 0; s < nst; s++) {
+      const float *xs = tile(buf, 0) + (wn * 32 + li) * kLS + 8 * h + (PAIRS ? 2 : 4) * rh;
+      const float *ws = tile(buf, 1) + (wm * 32 + li) * kLS + 8 * h + (PAIRS ? 2 : 4) * rh;
+      const int blocks = min(kKC / 16, nb - s * (kKC / 16));
+      // The next stage: this tile's s + 1, or the next tile's first.
+      const bool here = s + 1 < nst;
+      const bool more = here || has_next;
+      const int fs = here ? s + 1 : 0;
+      const int64_t fb = here ? b : nb_, fn0 = here ? n0 : nn0, fm0 = here ? m0 : nm0;
+      const BufOp &fbx = here ? bx : nbx;
+      const BufOp &fbw = here ? bw : nbw;
+      // As in dot_mfma8_k: straight-line blocks, block blk + 1's operands read
+      // (volatile, ahead of a scheduling barrier) before block blk's
+      // instructions issue; the next stage's loads after blocks 0 and 1, its
+      // LDS writes after blocks 4 and 5.
+      auto rd = [&](int k, float4 &x, float4 &w) {
+        const int o = 16 * (k < blocks ? k : blocks - 1);  // blocks >= 1 in every stage
+        if (PAIRS) {  // (x.x, x.y, x.z, x.w) = residues 2 rh, 2 rh + 1, 2 rh + 4, 2 rh + 5
+          const float2 xl = ld2_lds_v(xs + o), xh = ld2_lds_v(xs + o + 4);
+          const float2 wl = ld2_lds_v(ws + o), wh = ld2_lds_v(ws + o + 4);
+          x = make_float4(xl.x, xl.y, xh.x, xh.y);
+          w = make_float4(wl.x, wl.y, wh.x, wh.y);
+        } else {
+          x = ld4_lds_v(xs + o);
+          w = ld4_lds_v(ws + o);
+        }
+      };
+      auto part = [&](int q) {
+        if (more) {
+          if (q == 0) mfma_fetch<LX, TH>(X, fbx, fb, fn0, fs, nb, rx);
+          if (q == 1) mfma_fetch<LW, TH>(W, fbw, fb, fm0, fs, nb, rw);
+          if (q == 4) mfma_stash<LX, TH>(tile(buf ^ 1, 0), rx);
+          if (q == 5) mfma_stash<LW, TH>(tile(buf ^ 1, 1), rw);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      };
+      float4 pa, qa, pb, qb;  // set p: even blocks, set q: odd blocks
+      rd(0, pa, qa);
+#pragma unroll
+      for (int blk = 0; blk < kKC / 16; blk += 2) {
+        rd(blk + 1, pb, qb);
+        __builtin_amdgcn_sched_barrier(0);
+        if (blk < blocks) mfma_block4(acc, pa, qa);
+        if (blk == 0 || blk == 4) part(blk);
+        if (blk + 2 < kKC / 16) rd(blk + 2, pa, qa);
+        __builtin_amdgcn_sched_barrier(0);
+        if (blk + 1 < blocks) mfma_block4(acc, pb, qb);
+        if (blk == 0 || blk == 4) part(blk + 1);
+      }
+      __syncthreads();
+      buf ^= 1;
+    }
+
+    // Epilogue: register r of set q holds block r/16 of output row
+    // i = 8*((r%16)/4) + 4*h + r%4, column j = lane%32.  The exchange sits in
+    // the free stage buffer: [r][q][lane] per quadrant ([r][lane] with PAIRS).
+    float *xch = tile(buf ^ 1, 0) + quad * (16 * (PAIRS ? 1 : 4) * 64);
+    float pw[16][PAIRS ? 1 : 4];
+#pragma unroll
+    for (int r = 0; r < 16; r++) {
+      float t4[4];
+#pragma unroll
+      for (int q = 0; q < 4; q++) t4[q] = acc[q][r] + acc[q][r + 16];  // sum[0]+=sum[2] / sum[1]+=sum[3]
+      if (PAIRS) {
+        pw[r][0] = (t4[0] + t4[2]) + (t4[1] + t4[3]);  // sum[0]+=sum[1] for two lanes, then their pair
+      } else {
+#pragma unroll
+        for (int q = 0; q < 4; q++) pw[r][q] = t4[q];
+      }
+    }
+    constexpr int NV = PAIRS ? 1 : 4;
+    if (rh == 1) {
+#pragma unroll
+      for (int r = 0; r < 16; r++)
+#pragma unroll
+        for (int q = 0; q < NV; q++) xch[(r * NV + q) * 64 + lane] = pw[r][q];
+    }
+    __syncthreads();
+    if (rh == 0) {
+#pragma unroll
+      for (int r = 0; r < 16; r++) {
+        float sumf;
+        if (PAIRS) {
+          sumf = pw[r][0] + xch[r * 64 + lane];  // (w0 + w1) + (w2 + w3)
+        } else {
+          float w[4];
+#pragma unroll
+          for (int q = 0; q < 4; q++) w[q] = pw[r][q] + xch[(r * 4 + q) * 64 + lane];  // sum[0] += sum[1]
+          sumf = (w[0] + w[1]) + (w[2] + w[3]);                                      // vaddvq_f32
+        }
+        const int64_t n = n0 + wn * 32 + 8 * (r / 4) + 4 * h + (r % 4);
+        const int64_t m = m0 + wm * 32 + li;
+        if (n < N && m < M) {
+          if (np < K) {
+            const float *xr = X.p + b * X.sb + n * X.sf;
+            const float *wr = W.p + b * W.sb + m * W.sf;
+            if (tail == kTailPinned) {
+              for (int64_t k = np; k < K; k++) {
+                const float p = wr[k * W.sk] * xr[k * X.sk];
+                sumf = sumf + p;
+              }
+            } else {
+              const int64_t tl = K - np;
+              const int64_t nq = tl >= 4 ? (tl & ~(int64_t)3) : 0;
+              for (int64_t k = np; k < np + nq; k++) {
+                const float p = wr[k * W.sk] * xr[k * X.sk];
+                sumf = sumf + p;
+              }
+              for (int64_t k = np + nq; k < K; k++) sumf = __builtin_fmaf(wr[k * W.sk], xr[k * X.sk], sumf);
+            }
+          }
+          Y[(b * N + n) * M + m] = sumf;
+        }
+      }
+    }
+    __syncthreads();  // the exchange's buffer takes the stage after next's LDS writes
+    if (!has_next) break;
+    t = tn;
+    b = nb_;
+    n0 = nn0;
+    m0 = nm0;
+    bx = nbx;
+    bw = nbw;
+  }
+}
+
 constexpr int kDotLds = 2 * 2 * kMT * kLS * (int)sizeof(float);  // 135,168 bytes
-static_assert(4 * 16 * 4 * 64 * (int)sizeof(float) <= kDotLds, "the epilogue exchange fits the stage buffers");
+static_assert(4 * 16 * 4 * 64 <= 2 * kMT * kLS, "the epilogue exchange fits one stage buffer");
+constexpr int64_t kPersistStages = 4;
 
 // ---- soft_max ---------------------------------------------------------------------
 //
@@ -1014,6 +1209,8 @@ ArrayP dot_ggml(const DotOperand &lhs, const DotOperand &rhs, int64_t B, int64_t
     }
     static const bool lds_ok = [] {  // 135 KB of dynamic LDS, above the 64 KB default
 #define DOT_ATTR(a, c)                                                                                       \
+  SHLO_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(&dot_mfma8p_k<a, c, true>),                  \
+                               hipFuncAttributeMaxDynamicSharedMemorySize, kDotLds));                       \
   SHLO_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(&dot_mfma8_k<a, c>),                         \
                                hipFuncAttributeMaxDynamicSharedMemorySize, kDotLds));
       DOT_ATTR(kLoadRowVec, kLoadRowVec) DOT_ATTR(kLoadRowVec, kLoadColVec) DOT_ATTR(kLoadRowVec, kLoadScalar)
@@ -1030,15 +1227,25 @@ ArrayP dot_ggml(const DotOperand &lhs, const DotOperand &rhs, int64_t B, int64_t
     (void)lds_ok;
     const MfmaOperand X{L, lb, ln, lk, N}, W{R, rb, rm, rk, M};
     const int tiles_m = (int)((M + kMT - 1) / kMT);
-    const int64_t tiles = ((N + kMT - 1) / kMT) * tiles_m;
-    if (tiles > 0x7FFFFFFF) fail("dot_general: too many output tiles");
-    const dim3 grid((unsigned)tiles, (unsigned)B);
+    const int64_t tiles_b = ((N + kMT - 1) / kMT) * tiles_m, tiles = B * tiles_b;
+    if (tiles_m > 0x7FFFFFFF || tiles / std::max<int64_t>(B, 1) != tiles_b) fail("dot_general: too many output tiles");
+    // Short contractions (up to kPersistStages stages of 128) run the
+    // persistent kernel with the one-value exchange, whose next tile's loads
+    // hide under this tile's epilogue (attention 0.173 ms against 0.189 one
+    // workgroup per tile); long ones one workgroup per tile (config 3,
+    // K = 4096: 5.21 ms against 5.36 persistent).
+    const int64_t stages = (K / 16 + kKC / 16 - 1) / (kKC / 16);
+    const bool persist = stages <= kPersistStages;
+    const unsigned grid = (unsigned)std::min<int64_t>(tiles, device_props().multiProcessorCount);  // one per CU
+    const dim3 grid1((unsigned)tiles_b, (unsigned)B);
+    if (!persist && tiles_b > 0x7FFFFFFF) fail("dot_general: too many output tiles");
     const int tl = tail;
     launch([=](hipStream_t s) {
       (void)kl, (void)kr;
 #define DOT_CASE(a, c)                                                                    \
   if (lx == a && lw == c) {                                                               \
-    dot_mfma8_k<a, c><<<grid, 512, kDotLds, s>>>(X, W, N, M, K, tl, tiles_m, Y);         \
+    if (persist) dot_mfma8p_k<a, c, true><<<grid, 512, kDotLds, s>>>(X, W, N, M, K, tl, tiles_m, tiles_b, tiles, Y); \
+    else dot_mfma8_k<a, c><<<grid1, 512, kDotLds, s>>>(X, W, N, M, K, tl, tiles_m, Y);                  \
     return;                                                                               \
   }
       DOT_CASE(kLoadRowVec, kLoadRowVec) DOT_CASE(kLoadRowVec, kLoadColVec) DOT_CASE(kLoadRowVec, kLoadScalar)
