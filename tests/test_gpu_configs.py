@@ -101,6 +101,28 @@ def test_dot_batched_small(oracle):
         assert same_bits(got, want)
 
 
+@pytest.mark.parametrize("B,N,M,K", [(3, 700, 650, 100), (2, 1024, 1024, 512)])
+def test_dot_many_tiles(oracle, B, N, M, K):
+    """More output tiles than CUs, so workgroups of the short-contraction
+    kernel walk several tiles, across batch boundaries: (3,700,650,100) has
+    363 tiles with edge tiles, a short last stage and a 4-element tail (plain
+    loaders); (2,1024,1024,512) has 512 full tiles on the buffer loaders.
+    Both flavours, eager and compiled."""
+    import shlo_hip
+    lhs, st = oracle.fill_normal(31, 1.0, B * N * K)
+    rhs, _ = oracle.fill_normal(31, 1.0, B * K * M, state=st)
+    lhs, rhs = lhs.reshape(B, N, K), rhs.reshape(B, K, M)
+    for flavor in (0, 1):
+        want = oracle.dot_general_bnk(lhs, np.ascontiguousarray(rhs.transpose(0, 2, 1)), flavor)
+        shlo_hip.set_flavor(flavor)
+        try:
+            for compile in (True, False):
+                got = run(dot_module(N, K, M, batch=B), [lhs, rhs], compile=compile)[0]
+                assert same_bits(got, want), (flavor, compile)
+        finally:
+            shlo_hip.set_flavor(0)
+
+
 def causal_logits(oracle, rows, cols, sigma=4.0, seed=7):
     x, _ = oracle.fill_normal(seed, sigma, rows * cols)
     x = x.reshape(rows, cols)
