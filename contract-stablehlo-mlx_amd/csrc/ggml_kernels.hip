@@ -327,15 +327,55 @@ __device__ __forceinline__ float4 ld4_lds_v(const float *p) {
 // holds residues 4 rh .. 4 rh + 3 (block 0 of its four instructions) and
 // 4 rh + 8 .. 4 rh + 11 (block 1): 4 accumulator sets, 128 AGPRs.  Per block a
 // wave reads one float4 of each operand (k 16 b + 8 h + 4 rh ..) and issues 4
-// instructions.  In the epilogue the rh = 1 wave of each quadrant hands
-// a[4+q] + a[12+q] (q = 0..3, GGML_F32x4_REDUCE's sum[1] += sum[3]) through LDS
-// to the rh = 0 wave, which holds a[q] + a[8+q] (sum[0] += sum[2]) and finishes
-// the tree, the tail and the store.
+// instructions.  In the epilogue the rh = 0 wave holds a[q] + a[8+q] (q = 0..3,
+// GGML_F32x4_REDUCE's sum[0] += sum[2]) and the rh = 1 wave a[4+q] + a[12+q]
+// (sum[1] += sum[3]); each hands the other the four values of the rows the
+// other finishes (tree, tail and store): rows 0..7 of the quadrant's 16 per
+// lane go to rh = 0, rows 8..15 to rh = 1.
 __device__ __forceinline__ void mfma_block4(v32f (&acc)[4], const float4 &a, const float4 &b) {
   acc[0] = __builtin_amdgcn_mfma_f32_32x32x1f32(a.x, b.x, acc[0], 0, 0, 0);
   acc[1] = __builtin_amdgcn_mfma_f32_32x32x1f32(a.y, b.y, acc[1], 0, 0, 0);
   acc[2] = __builtin_amdgcn_mfma_f32_32x32x1f32(a.z, b.z, acc[2], 0, 0, 0);
   acc[3] = __builtin_amdgcn_mfma_f32_32x32x1f32(a.w, b.w, acc[3], 0, 0, 0);
+}
+
+// Stores the 8 outputs a lane finishes: rows n + 8 (r / 4) + r % 4 of column m
+// (r = 0..7), after the serial tail of dot_finish when K % 16 != 0.  `whole`
+// (wave-uniform) says every output is in range and there is no tail.
+__device__ __forceinline__ void dot_store_rows(const MfmaOperand &X, const MfmaOperand &W, int64_t b, int64_t n,
+                                               int64_t m, int64_t N, int64_t M, int64_t K, int64_t np, int tail,
+                                               bool whole, const float (&out)[8], float *__restrict__ Y) {
+  float *y = Y + (b * N + n) * M + m;
+  if (whole) {
+#pragma unroll
+    for (int r = 0; r < 8; r++) y[(8 * (r / 4) + r % 4) * M] = out[r];
+    return;
+  }
+#pragma unroll
+  for (int r = 0; r < 8; r++) {
+    const int64_t nr = n + 8 * (r / 4) + r % 4;
+    if (nr >= N || m >= M) continue;
+    float sumf = out[r];
+    if (np < K) {
+      const float *xr = X.p + b * X.sb + nr * X.sf;
+      const float *wr = W.p + b * W.sb + m * W.sf;
+      if (tail == kTailPinned) {
+        for (int64_t k = np; k < K; k++) {
+          const float p = wr[k * W.sk] * xr[k * X.sk];
+          sumf = sumf + p;
+        }
+      } else {
+        const int64_t tl = K - np;
+        const int64_t nq = tl >= 4 ? (tl & ~(int64_t)3) : 0;
+        for (int64_t k = np; k < np + nq; k++) {
+          const float p = wr[k * W.sk] * xr[k * X.sk];
+          sumf = sumf + p;
+        }
+        for (int64_t k = np + nq; k < K; k++) sumf = __builtin_fmaf(wr[k * W.sk], xr[k * X.sk], sumf);
+      }
+    }
+    y[(8 * (r / 4) + r % 4) * M] = sumf;
+  }
 }
 
 template <int LX, int LW>
@@ -416,46 +456,34 @@ __global__ void __launch_bounds__(512) dot_mfma8_k(MfmaOperand X, MfmaOperand W,
   }
 
   // Epilogue: register r of set q holds block r/16 of output row
-  // i = 8*((r%16)/4) + 4*h + r%4, column j = lane%32.
-  float *xch = lds_m + quad * (16 * 4 * 64);  // [r][q][lane]
-  if (rh == 1) {
+  // i = 8*((r%16)/4) + 4*h + r%4, column j = lane%32.  Wave half rh finishes
+  // rows r in [8 rh, 8 rh + 8) of its quadrant and hands the other half its
+  // partial sums for the rest through LDS (every wave stores).
+  float t4[16][4];
 #pragma unroll
-    for (int r = 0; r < 16; r++)
+  for (int r = 0; r < 16; r++)
 #pragma unroll
-      for (int q = 0; q < 4; q++) xch[(r * 4 + q) * 64 + lane] = acc[q][r] + acc[q][r + 16];  // sum[1] += sum[3]
-  }
+    for (int q = 0; q < 4; q++) t4[r][q] = acc[q][r] + acc[q][r + 16];  // rh 0: sum[0] += sum[2]; rh 1: sum[1] += sum[3]
+  float *give = lds_m + wave * (8 * 4 * 64);                            // [r % 8][q][lane]
+  const float *take = lds_m + (wave ^ 4) * (8 * 4 * 64);
+#pragma unroll
+  for (int r = 0; r < 8; r++)
+#pragma unroll
+    for (int q = 0; q < 4; q++) give[(r * 4 + q) * 64 + lane] = rh ? t4[r][q] : t4[8 + r][q];
   __syncthreads();
-  if (rh == 1) return;
+  float out[8];
 #pragma unroll
-  for (int r = 0; r < 16; r++) {
+  for (int r = 0; r < 8; r++) {
     float w[4];
 #pragma unroll
-    for (int q = 0; q < 4; q++) w[q] = (acc[q][r] + acc[q][r + 16]) + xch[(r * 4 + q) * 64 + lane];  // sum[0]+=sum[2], +=sum[1]
-    float sumf = (w[0] + w[1]) + (w[2] + w[3]);                                                    // vaddvq_f32
-    const int64_t n = n0 + wn * 32 + 8 * (r / 4) + 4 * h + (r % 4);
-    const int64_t m = m0 + wm * 32 + li;
-    if (n < N && m < M) {
-      if (np < K) {
-        const float *xr = X.p + b * X.sb + n * X.sf;
-        const float *wr = W.p + b * W.sb + m * W.sf;
-        if (tail == kTailPinned) {
-          for (int64_t k = np; k < K; k++) {
-            const float p = wr[k * W.sk] * xr[k * X.sk];
-            sumf = sumf + p;
-          }
-        } else {
-          const int64_t tl = K - np;
-          const int64_t nq = tl >= 4 ? (tl & ~(int64_t)3) : 0;
-          for (int64_t k = np; k < np + nq; k++) {
-            const float p = wr[k * W.sk] * xr[k * X.sk];
-            sumf = sumf + p;
-          }
-          for (int64_t k = np + nq; k < K; k++) sumf = __builtin_fmaf(wr[k * W.sk], xr[k * X.sk], sumf);
-        }
-      }
-      Y[(b * N + n) * M + m] = sumf;
+    for (int q = 0; q < 4; q++) {
+      const float mine = rh ? t4[8 + r][q] : t4[r][q], other = take[(r * 4 + q) * 64 + lane];
+      w[q] = rh ? other + mine : mine + other;  // sum[0] += sum[1]
     }
+    out[r] = (w[0] + w[1]) + (w[2] + w[3]);  // vaddvq_f32
   }
+  dot_store_rows(X, W, b, n0 + wn * 32 + 4 * h + 16 * rh, m0 + wm * 32 + li, N, M, K, np, tail,
+                 np == K && n0 + kMT <= N && m0 + kMT <= M, out, Y);
 }
 
 typedef float f32x2 __attribute__((ext_vector_type(2)));
@@ -475,17 +503,15 @@ __device__ __forceinline__ float2 ld2_lds_v(const float *p) {
 // LDS writes out of it until the exchange has been read.  Tiles run
 // round-robin, so the workgroups that share an rhs tile at one time sit on one
 // XCD (for 4 row tiles per rhs tile).
-// PAIRS = false splits the chains as dot_mfma8_k does (one float4 of each
-// operand per block, four values per output exchanged).  PAIRS = true gives
-// the rh = 0 wave the residue pairs (r, r + 8) for r in {0, 1, 4, 5} and the
-// rh = 1 wave r in {2, 3, 6, 7}: each finishes w_r = (a[r] + a[r+8]) +
-// (a[r+4] + a[r+12]) for two r of GGML_F32x4_REDUCE and adds its pair,
-// (w0 + w1) or (w2 + w3), so one value per output crosses for vaddvq_f32's
-// (w0 + w1) + (w2 + w3); a block then takes two float2 of each operand
-// (k 16 b + 8 h + 2 rh and + 4).  The smaller exchange pays where the
-// epilogue is a large share of a tile (short K); the float4 reads where it is
-// not.
-template <int LX, int LW, bool PAIRS>
+// The chains split by residue pairs: the rh = 0 wave holds (r, r + 8) for r
+// in {0, 1, 4, 5} and the rh = 1 wave r in {2, 3, 6, 7}; each finishes
+// w_r = (a[r] + a[r+8]) + (a[r+4] + a[r+12]) for two r of GGML_F32x4_REDUCE and
+// adds its pair, (w0 + w1) or (w2 + w3), so one value per output crosses for
+// vaddvq_f32's (w0 + w1) + (w2 + w3), and each wave half finishes and stores
+// half of the rows.  A block takes two float2 of each operand (k 16 b + 8 h +
+// 2 rh and + 4).  The smaller exchange pays where the epilogue is a large
+// share of a tile (short K); dot_mfma8_k's float4 reads where it is not.
+template <int LX, int LW>
 __global__ void __launch_bounds__(512) dot_mfma8p_k(MfmaOperand X, MfmaOperand W, int64_t N, int64_t M, int64_t K,
                                                     int tail, int tiles_m, int64_t tiles_b, int64_t tiles,
                                                     float *__restrict__ Y) {
@@ -527,8 +553,8 @@ __global__ void __launch_bounds__(512) dot_mfma8p_k(MfmaOperand X, MfmaOperand W
                   nm0 = has_next ? tile_m0(tn) : m0;
     const BufOp nbx = buf_op<LX>(X, nb_, nn0), nbw = buf_op<LW>(W, nb_, nm0);
     for (int s = 0; s < nst; s++) {
-      const float *xs = tile(buf, 0) + (wn * 32 + li) * kLS + 8 * h + (PAIRS ? 2 : 4) * rh;
-      const float *ws = tile(buf, 1) + (wm * 32 + li) * kLS + 8 * h + (PAIRS ? 2 : 4) * rh;
+      const float *xs = tile(buf, 0) + (wn * 32 + li) * kLS + 8 * h + 2 * rh;
+      const float *ws = tile(buf, 1) + (wm * 32 + li) * kLS + 8 * h + 2 * rh;
       const int blocks = min(kKC / 16, nb - s * (kKC / 16));
       // The next stage: this tile's s + 1, or the next tile's first.
       const bool here = s + 1 < nst;
@@ -543,15 +569,11 @@ __global__ void __launch_bounds__(512) dot_mfma8p_k(MfmaOperand X, MfmaOperand W
       // LDS writes after blocks 4 and 5.
       auto rd = [&](int k, float4 &x, float4 &w) {
         const int o = 16 * (k < blocks ? k : blocks - 1);  // blocks >= 1 in every stage
-        if (PAIRS) {  // (x.x, x.y, x.z, x.w) = residues 2 rh, 2 rh + 1, 2 rh + 4, 2 rh + 5
-          const float2 xl = ld2_lds_v(xs + o), xh = ld2_lds_v(xs + o + 4);
-          const float2 wl = ld2_lds_v(ws + o), wh = ld2_lds_v(ws + o + 4);
-          x = make_float4(xl.x, xl.y, xh.x, xh.y);
-          w = make_float4(wl.x, wl.y, wh.x, wh.y);
-        } else {
-          x = ld4_lds_v(xs + o);
-          w = ld4_lds_v(ws + o);
-        }
+        // (x.x, x.y, x.z, x.w) = residues 2 rh, 2 rh + 1, 2 rh + 4, 2 rh + 5
+        const float2 xl = ld2_lds_v(xs + o), xh = ld2_lds_v(xs + o + 4);
+        const float2 wl = ld2_lds_v(ws + o), wh = ld2_lds_v(ws + o + 4);
+        x = make_float4(xl.x, xl.y, xh.x, xh.y);
+        w = make_float4(wl.x, wl.y, wh.x, wh.y);
       };
       auto part = [&](int q) {
         if (more) {
@@ -580,67 +602,30 @@ __global__ void __launch_bounds__(512) dot_mfma8p_k(MfmaOperand X, MfmaOperand W
     }
 
     // Epilogue: register r of set q holds block r/16 of output row
-    // i = 8*((r%16)/4) + 4*h + r%4, column j = lane%32.  The exchange sits in
-    // the free stage buffer: [r][q][lane] per quadrant ([r][lane] with PAIRS).
-    float *xch = tile(buf ^ 1, 0) + quad * (16 * (PAIRS ? 1 : 4) * 64);
-    float pw[16][PAIRS ? 1 : 4];
+    // i = 8*((r%16)/4) + 4*h + r%4, column j = lane%32.  Wave half rh finishes
+    // rows r in [8 rh, 8 rh + 8) and hands the other half its pair sums for
+    // the rest, through the free stage buffer ([r % 8][lane] per wave).
+    float pw[16];
 #pragma unroll
     for (int r = 0; r < 16; r++) {
       float t4[4];
 #pragma unroll
       for (int q = 0; q < 4; q++) t4[q] = acc[q][r] + acc[q][r + 16];  // sum[0]+=sum[2] / sum[1]+=sum[3]
-      if (PAIRS) {
-        pw[r][0] = (t4[0] + t4[2]) + (t4[1] + t4[3]);  // sum[0]+=sum[1] for two lanes, then their pair
-      } else {
-#pragma unroll
-        for (int q = 0; q < 4; q++) pw[r][q] = t4[q];
-      }
+      pw[r] = (t4[0] + t4[2]) + (t4[1] + t4[3]);  // sum[0]+=sum[1] for two lanes, then their pair
     }
-    constexpr int NV = PAIRS ? 1 : 4;
-    if (rh == 1) {
+    float *give = tile(buf ^ 1, 0) + wave * (8 * 64);
+    const float *take = tile(buf ^ 1, 0) + (wave ^ 4) * (8 * 64);
 #pragma unroll
-      for (int r = 0; r < 16; r++)
-#pragma unroll
-        for (int q = 0; q < NV; q++) xch[(r * NV + q) * 64 + lane] = pw[r][q];
-    }
+    for (int r = 0; r < 8; r++) give[r * 64 + lane] = rh ? pw[r] : pw[8 + r];
     __syncthreads();
-    if (rh == 0) {
+    float out[8];
 #pragma unroll
-      for (int r = 0; r < 16; r++) {
-        float sumf;
-        if (PAIRS) {
-          sumf = pw[r][0] + xch[r * 64 + lane];  // (w0 + w1) + (w2 + w3)
-        } else {
-          float w[4];
-#pragma unroll
-          for (int q = 0; q < 4; q++) w[q] = pw[r][q] + xch[(r * 4 + q) * 64 + lane];  // sum[0] += sum[1]
-          sumf = (w[0] + w[1]) + (w[2] + w[3]);                                      // vaddvq_f32
-        }
-        const int64_t n = n0 + wn * 32 + 8 * (r / 4) + 4 * h + (r % 4);
-        const int64_t m = m0 + wm * 32 + li;
-        if (n < N && m < M) {
-          if (np < K) {
-            const float *xr = X.p + b * X.sb + n * X.sf;
-            const float *wr = W.p + b * W.sb + m * W.sf;
-            if (tail == kTailPinned) {
-              for (int64_t k = np; k < K; k++) {
-                const float p = wr[k * W.sk] * xr[k * X.sk];
-                sumf = sumf + p;
-              }
-            } else {
-              const int64_t tl = K - np;
-              const int64_t nq = tl >= 4 ? (tl & ~(int64_t)3) : 0;
-              for (int64_t k = np; k < np + nq; k++) {
-                const float p = wr[k * W.sk] * xr[k * X.sk];
-                sumf = sumf + p;
-              }
-              for (int64_t k = np + nq; k < K; k++) sumf = __builtin_fmaf(wr[k * W.sk], xr[k * X.sk], sumf);
-            }
-          }
-          Y[(b * N + n) * M + m] = sumf;
-        }
-      }
+    for (int r = 0; r < 8; r++) {
+      const float mine = rh ? pw[8 + r] : pw[r], other = take[r * 64 + lane];
+      out[r] = rh ? other + mine : mine + other;  // (w0 + w1) + (w2 + w3)
     }
+    dot_store_rows(X, W, b, n0 + wn * 32 + 4 * h + 16 * rh, m0 + wm * 32 + li, N, M, K, np, tail,
+                   np == K && n0 + kMT <= N && m0 + kMT <= M, out, Y);
     __syncthreads();  // the exchange's buffer takes the stage after next's LDS writes
     if (!has_next) break;
     t = tn;
@@ -653,7 +638,8 @@ __global__ void __launch_bounds__(512) dot_mfma8p_k(MfmaOperand X, MfmaOperand W
 }
 
 constexpr int kDotLds = 2 * 2 * kMT * kLS * (int)sizeof(float);  // 135,168 bytes
-static_assert(4 * 16 * 4 * 64 <= 2 * kMT * kLS, "the epilogue exchange fits one stage buffer");
+static_assert(8 * 8 * 64 <= 2 * kMT * kLS, "the persistent epilogue's exchange fits one stage buffer");
+static_assert(8 * 8 * 4 * 64 <= 4 * kMT * kLS, "dot_mfma8_k's epilogue exchange fits the LDS");
 constexpr int64_t kPersistStages = 4;
 
 // ---- soft_max ---------------------------------------------------------------------
@@ -1209,7 +1195,7 @@ ArrayP dot_ggml(const DotOperand &lhs, const DotOperand &rhs, int64_t B, int64_t
     }
     static const bool lds_ok = [] {  // 135 KB of dynamic LDS, above the 64 KB default
 #define DOT_ATTR(a, c)                                                                                       \
-  SHLO_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(&dot_mfma8p_k<a, c, true>),                  \
+  SHLO_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(&dot_mfma8p_k<a, c>),                        \
                                hipFuncAttributeMaxDynamicSharedMemorySize, kDotLds));                       \
   SHLO_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(&dot_mfma8_k<a, c>),                         \
                                hipFuncAttributeMaxDynamicSharedMemorySize, kDotLds));
@@ -1244,7 +1230,7 @@ ArrayP dot_ggml(const DotOperand &lhs, const DotOperand &rhs, int64_t B, int64_t
       (void)kl, (void)kr;
 #define DOT_CASE(a, c)                                                                    \
   if (lx == a && lw == c) {                                                               \
-    if (persist) dot_mfma8p_k<a, c, true><<<grid, 512, kDotLds, s>>>(X, W, N, M, K, tl, tiles_m, tiles_b, tiles, Y); \
+    if (persist) dot_mfma8p_k<a, c><<<grid, 512, kDotLds, s>>>(X, W, N, M, K, tl, tiles_m, tiles_b, tiles, Y); \
     else dot_mfma8_k<a, c><<<grid1, 512, kDotLds, s>>>(X, W, N, M, K, tl, tiles_m, Y);                  \
     return;                                                                               \
   }
