@@ -1,0 +1,102 @@
+// Element-wise binary32 operations and the fused epilogue a producing kernel
+// (dot_general, norm) applies to each output before it stores it.
+//
+// A StableHLO add / subtract / multiply / divide / maximum / minimum is one
+// correctly rounded IEEE operation per element (Lower.lean:13-17, :375-452),
+// so applying it to a value in registers right after the producing kernel
+// computed it gives the same bits as the separate element-wise kernel reading
+// the stored value back: f32_binary below is the one definition both use.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdint>
+
+#include "ops.h"
+
+namespace shlo {
+
+// Binary32 semantics of the arithmetic binary op codes
+// (StablehloMlx/Mlx.lean:286-307): maximum / minimum order -0 below +0
+// (mx::maximum).  A NaN operand propagates as on arm64 and x86 (the first
+// NaN operand, quieted, sign kept): the result is x + y, which the GPU's add
+// returns that way, where its subtract would flip a NaN's sign.
+__host__ __device__ inline float f32_binary(uint32_t op, float x, float y) {
+  if (x != x || y != y) return x + y;
+  switch (op) {
+    case kAdd: return x + y;
+    case kSub: return x - y;
+    case kMul: return x * y;
+    case kDiv: return x / y;  // correctly rounded: built with -fhip-fp32-correctly-rounded-divide-sqrt
+    case kMax:
+      if (x == y) return std::signbit(x) ? y : x;
+      return x > y ? x : y;
+    case kMin:
+      if (x == y) return std::signbit(x) ? x : y;
+      return x < y ? x : y;
+    default: return x;
+  }
+}
+
+// Up to kMaxEpi binary ops applied in order to an output value v at index
+// (i0, i1, i2) of the producer's output: v = op(v, p[i0*s0 + i1*s1 + i2*s2]),
+// or op(p[...], v) when `rev` (the produced value was the op's right operand).
+struct EpiOp {
+  const float *p;
+  int64_t s0, s1, s2;
+  uint32_t code, rev;
+};
+struct Epilogue {
+  EpiOp op[kMaxEpi];
+  int n = 0;
+};
+
+__device__ __forceinline__ float epi_apply(const Epilogue &e, float v, int64_t i0, int64_t i1, int64_t i2) {
+#pragma unroll
+  for (int k = 0; k < kMaxEpi; k++) {
+    if (k < e.n) {
+      const EpiOp &o = e.op[k];
+      const float w = o.p[i0 * o.s0 + i1 * o.s1 + i2 * o.s2];
+      v = o.rev ? f32_binary(o.code, w, v) : f32_binary(o.code, v, w);
+    }
+  }
+  return v;
+}
+
+// The fused ops on the 8 outputs a lane of the matrix kernels finishes: rows
+// n + 8 (r / 4) + r % 4 (r = 0..7, each clamped to nmax so a discarded row
+// reads in range) of column m in batch b.  One uniform switch per op, then the
+// op on all 8 values.
+template <uint32_t C>
+__device__ __forceinline__ void epi_op8(float (&v)[8], const float (&w)[8], uint32_t rev) {
+#pragma unroll
+  for (int r = 0; r < 8; r++) v[r] = rev ? f32_binary(C, w[r], v[r]) : f32_binary(C, v[r], w[r]);
+}
+
+__device__ __forceinline__ void epi_rows8(const Epilogue &e, float (&v)[8], int64_t b, int64_t n, int64_t nmax,
+                                          int64_t m) {
+#pragma unroll
+  for (int k = 0; k < kMaxEpi; k++) {
+    if (k >= e.n) break;
+    const EpiOp &o = e.op[k];
+    const float *p = o.p + b * o.s0 + m * o.s2;
+    float w[8];
+#pragma unroll
+    for (int r = 0; r < 8; r++) {
+      const int64_t nr = n + 8 * (r / 4) + r % 4;
+      w[r] = p[(nr < nmax ? nr : nmax) * o.s1];
+    }
+    switch (o.code) {
+      case kAdd: epi_op8<kAdd>(v, w, o.rev); break;
+      case kSub: epi_op8<kSub>(v, w, o.rev); break;
+      case kMul: epi_op8<kMul>(v, w, o.rev); break;
+      case kDiv: epi_op8<kDiv>(v, w, o.rev); break;
+      case kMax: epi_op8<kMax>(v, w, o.rev); break;
+      case kMin: epi_op8<kMin>(v, w, o.rev); break;
+      default: break;
+    }
+  }
+}
+
+}  // namespace shlo

@@ -7,6 +7,7 @@
 
 #include <type_traits>
 
+#include "epilogue.h"
 #include "erff_cr.h"
 #include "expf_cr.h"
 #include "ggml_expf.h"
@@ -87,7 +88,7 @@ template <int TAIL>
 __global__ void __launch_bounds__(256) dot_ggml_simple(int64_t n_out, int64_t N, int64_t M, int64_t K,
                                                        const float *__restrict__ L, int64_t lb, int64_t ln, int64_t lk,
                                                        const float *__restrict__ R, int64_t rb, int64_t rm, int64_t rk,
-                                                       float *__restrict__ y) {
+                                                       Epilogue ep, float *__restrict__ y) {
   for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n_out; i += (int64_t)gridDim.x * blockDim.x) {
     const int64_t m = i % M, t = i / M, n = t % N, b = t / N;
     const float *x = L + b * lb + n * ln;
@@ -98,7 +99,7 @@ __global__ void __launch_bounds__(256) dot_ggml_simple(int64_t n_out, int64_t N,
         const float p = w[k * rk] * x[k * lk];
         s = s + p;
       }
-      y[i] = s;
+      y[i] = epi_apply(ep, s, b, n, m);
       continue;
     }
     float a[16];
@@ -109,7 +110,7 @@ __global__ void __launch_bounds__(256) dot_ggml_simple(int64_t n_out, int64_t N,
 #pragma unroll
       for (int j = 0; j < 16; j++) a[j] = __builtin_fmaf(w[(k0 + j) * rk], x[(k0 + j) * lk], a[j]);
     }
-    y[i] = dot_finish<TAIL>(a, w, rk, x, lk, np, K);
+    y[i] = epi_apply(ep, dot_finish<TAIL>(a, w, rk, x, lk, np, K), b, n, m);
   }
 }
 
@@ -340,25 +341,24 @@ __device__ __forceinline__ void mfma_block4(v32f (&acc)[4], const float4 &a, con
 }
 
 // Stores the 8 outputs a lane finishes: rows n + 8 (r / 4) + r % 4 of column m
-// (r = 0..7), after the serial tail of dot_finish when K % 16 != 0.  `whole`
-// (wave-uniform) says every output is in range and there is no tail.
+// (r = 0..7), after the serial tail of dot_finish when K % 16 != 0 and the
+// fused element-wise ops.  `whole` (wave-uniform) says every output is in
+// range and there is no tail.
 __device__ __forceinline__ void dot_store_rows(const MfmaOperand &X, const MfmaOperand &W, int64_t b, int64_t n,
                                                int64_t m, int64_t N, int64_t M, int64_t K, int64_t np, int tail,
-                                               bool whole, const float (&out)[8], float *__restrict__ Y) {
-  float *y = Y + (b * N + n) * M + m;
-  if (whole) {
+                                               bool whole, const float (&out)[8], const Epilogue &ep,
+                                               float *__restrict__ Y) {
+  float v[8];
 #pragma unroll
-    for (int r = 0; r < 8; r++) y[(8 * (r / 4) + r % 4) * M] = out[r];
-    return;
-  }
+  for (int r = 0; r < 8; r++) v[r] = out[r];
+  if (!whole && np < K && m < M) {
 #pragma unroll
-  for (int r = 0; r < 8; r++) {
-    const int64_t nr = n + 8 * (r / 4) + r % 4;
-    if (nr >= N || m >= M) continue;
-    float sumf = out[r];
-    if (np < K) {
+    for (int r = 0; r < 8; r++) {
+      const int64_t nr = n + 8 * (r / 4) + r % 4;
+      if (nr >= N) continue;
       const float *xr = X.p + b * X.sb + nr * X.sf;
       const float *wr = W.p + b * W.sb + m * W.sf;
+      float sumf = v[r];
       if (tail == kTailPinned) {
         for (int64_t k = np; k < K; k++) {
           const float p = wr[k * W.sk] * xr[k * X.sk];
@@ -373,14 +373,25 @@ __device__ __forceinline__ void dot_store_rows(const MfmaOperand &X, const MfmaO
         }
         for (int64_t k = np + nq; k < K; k++) sumf = __builtin_fmaf(wr[k * W.sk], xr[k * X.sk], sumf);
       }
+      v[r] = sumf;
     }
-    y[(8 * (r / 4) + r % 4) * M] = sumf;
   }
+  if (ep.n > 0) epi_rows8(ep, v, b, n, N - 1, m < M ? m : M - 1);
+  float *y = Y + (b * N + n) * M + m;
+  if (whole) {
+#pragma unroll
+    for (int r = 0; r < 8; r++) y[(8 * (r / 4) + r % 4) * M] = v[r];
+    return;
+  }
+  if (m >= M) return;
+#pragma unroll
+  for (int r = 0; r < 8; r++)
+    if (n + 8 * (r / 4) + r % 4 < N) y[(8 * (r / 4) + r % 4) * M] = v[r];
 }
 
 template <int LX, int LW>
 __global__ void __launch_bounds__(512) dot_mfma8_k(MfmaOperand X, MfmaOperand W, int64_t N, int64_t M, int64_t K,
-                                                   int tail, int tiles_m, float *__restrict__ Y) {
+                                                   int tail, int tiles_m, Epilogue ep, float *__restrict__ Y) {
   constexpr int TH = 512, R = regs_of<TH>();
   extern __shared__ float lds_m[];  // [buffer][operand][kMT * kLS]; the epilogue's exchange reuses it
   auto tile = [&](int buf, int op) { return lds_m + (buf * 2 + op) * (kMT * kLS); };
@@ -483,7 +494,7 @@ __global__ void __launch_bounds__(512) dot_mfma8_k(MfmaOperand X, MfmaOperand W,
     out[r] = (w[0] + w[1]) + (w[2] + w[3]);  // vaddvq_f32
   }
   dot_store_rows(X, W, b, n0 + wn * 32 + 4 * h + 16 * rh, m0 + wm * 32 + li, N, M, K, np, tail,
-                 np == K && n0 + kMT <= N && m0 + kMT <= M, out, Y);
+                 np == K && n0 + kMT <= N && m0 + kMT <= M, out, ep, Y);
 }
 
 typedef float f32x2 __attribute__((ext_vector_type(2)));
@@ -514,7 +525,7 @@ __device__ __forceinline__ float2 ld2_lds_v(const float *p) {
 template <int LX, int LW>
 __global__ void __launch_bounds__(512) dot_mfma8p_k(MfmaOperand X, MfmaOperand W, int64_t N, int64_t M, int64_t K,
                                                     int tail, int tiles_m, int64_t tiles_b, int64_t tiles,
-                                                    float *__restrict__ Y) {
+                                                    Epilogue ep, float *__restrict__ Y) {
   constexpr int TH = 512, R = regs_of<TH>();
   extern __shared__ float lds_m[];  // [buffer][operand][kMT * kLS]
   auto tile = [&](int buf, int op) { return lds_m + (buf * 2 + op) * (kMT * kLS); };
@@ -625,7 +636,7 @@ __global__ void __launch_bounds__(512) dot_mfma8p_k(MfmaOperand X, MfmaOperand W
       out[r] = rh ? other + mine : mine + other;  // (w0 + w1) + (w2 + w3)
     }
     dot_store_rows(X, W, b, n0 + wn * 32 + 4 * h + 16 * rh, m0 + wm * 32 + li, N, M, K, np, tail,
-                   np == K && n0 + kMT <= N && m0 + kMT <= M, out, Y);
+                   np == K && n0 + kMT <= N && m0 + kMT <= M, out, ep, Y);
     __syncthreads();  // the exchange's buffer takes the stage after next's LDS writes
     if (!has_next) break;
     t = tn;
@@ -1158,9 +1169,23 @@ void set_default_dot_tail(int t) {
   g_default_tail = t;
 }
 
-ArrayP dot_ggml(const DotOperand &lhs, const DotOperand &rhs, int64_t B, int64_t N, int64_t M, int64_t K, int tail) {
+Epilogue make_epilogue(const std::vector<FusedOp> &ops, std::vector<ArrayP> *keep) {
+  if (ops.size() > (size_t)kMaxEpi) fail(strf("fused epilogue: at most %d ops", kMaxEpi));
+  Epilogue ep;
+  for (const FusedOp &o : ops) {
+    if (!o.arr || o.arr->dtype != kF32 || !o.arr->buf) fail("fused epilogue: f32 operands only");
+    ep.op[ep.n++] = EpiOp{(const float *)o.arr->data(), o.s0, o.s1, o.s2, o.code, o.rev ? 1u : 0u};
+    keep->push_back(o.arr);
+  }
+  return ep;
+}
+
+ArrayP dot_ggml(const DotOperand &lhs, const DotOperand &rhs, int64_t B, int64_t N, int64_t M, int64_t K, int tail,
+                const std::vector<FusedOp> &epi) {
   if (lhs.arr->dtype != kF32 || rhs.arr->dtype != kF32) fail("dot_general: f32 operands only");
   if (B < 0 || N < 0 || M < 0 || K < 0) fail("dot_general: negative extent");
+  std::vector<ArrayP> ek;
+  const Epilogue ep = make_epilogue(epi, &ek);
   auto y = new_array(kF32, Shape{B * N * M});
   const int64_t n_out = B * N * M;
   if (n_out == 0) return y;
@@ -1227,11 +1252,11 @@ ArrayP dot_ggml(const DotOperand &lhs, const DotOperand &rhs, int64_t B, int64_t
     if (!persist && tiles_b > 0x7FFFFFFF) fail("dot_general: too many output tiles");
     const int tl = tail;
     launch([=](hipStream_t s) {
-      (void)kl, (void)kr;
+      (void)kl, (void)kr, (void)ek;
 #define DOT_CASE(a, c)                                                                    \
   if (lx == a && lw == c) {                                                               \
-    if (persist) dot_mfma8p_k<a, c><<<grid, 512, kDotLds, s>>>(X, W, N, M, K, tl, tiles_m, tiles_b, tiles, Y); \
-    else dot_mfma8_k<a, c><<<grid1, 512, kDotLds, s>>>(X, W, N, M, K, tl, tiles_m, Y);                  \
+    if (persist) dot_mfma8p_k<a, c><<<grid, 512, kDotLds, s>>>(X, W, N, M, K, tl, tiles_m, tiles_b, tiles, ep, Y); \
+    else dot_mfma8_k<a, c><<<grid1, 512, kDotLds, s>>>(X, W, N, M, K, tl, tiles_m, ep, Y);                  \
     return;                                                                               \
   }
       DOT_CASE(kLoadRowVec, kLoadRowVec) DOT_CASE(kLoadRowVec, kLoadColVec) DOT_CASE(kLoadRowVec, kLoadScalar)
@@ -1248,16 +1273,16 @@ ArrayP dot_ggml(const DotOperand &lhs, const DotOperand &rhs, int64_t B, int64_t
   }
   const unsigned grid = grid_cap(n_out, 256, 1 << 20);
   launch([=](hipStream_t s) {
-    (void)kl, (void)kr;
+    (void)kl, (void)kr, (void)ek;
     switch (tail) {
       case kTailStock:
-        dot_ggml_simple<kTailStock><<<grid, 256, 0, s>>>(n_out, N, M, K, L, lb, ln, lk, R, rb, rm, rk, Y);
+        dot_ggml_simple<kTailStock><<<grid, 256, 0, s>>>(n_out, N, M, K, L, lb, ln, lk, R, rb, rm, rk, ep, Y);
         break;
       case kTailPinned:
-        dot_ggml_simple<kTailPinned><<<grid, 256, 0, s>>>(n_out, N, M, K, L, lb, ln, lk, R, rb, rm, rk, Y);
+        dot_ggml_simple<kTailPinned><<<grid, 256, 0, s>>>(n_out, N, M, K, L, lb, ln, lk, R, rb, rm, rk, ep, Y);
         break;
       default:
-        dot_ggml_simple<kTailPlain><<<grid, 256, 0, s>>>(n_out, N, M, K, L, lb, ln, lk, R, rb, rm, rk, Y);
+        dot_ggml_simple<kTailPlain><<<grid, 256, 0, s>>>(n_out, N, M, K, L, lb, ln, lk, R, rb, rm, rk, ep, Y);
         break;
     }
   });

@@ -202,7 +202,55 @@ DotOperand dot_operand(const ArrayP &a, const std::vector<int64_t> &batch, const
   return op;
 }
 
-ArrayP dot_general(const Faults &f, const Op &o, const ArrayP &a, const ArrayP &b) {  // Lower.lean:157-182
+// An element-wise op that follows a producer: `other` is its second operand,
+// `rev` says the produced value is its right operand.
+struct Chained {
+  uint32_t code;
+  bool rev;
+  ArrayP other;
+};
+
+// Applies the chain's ops from `from` on as separate element-wise kernels.
+ArrayP apply_chain(ArrayP v, const std::vector<Chained> &chain, size_t from) {
+  for (size_t i = from; i < chain.size(); i++)
+    v = chain[i].rev ? binary(chain[i].code, chain[i].other, v) : binary(chain[i].code, v, chain[i].other);
+  return v;
+}
+
+// The chain's leading ops that a producer with output index (i0, i1, i2) over
+// the dim groups g0, g1, g2 of `dims` can fuse: each other operand f32 of
+// shape `dims`, its strides flat over every group.
+std::vector<FusedOp> fusable_prefix(const std::vector<Chained> &chain, const Shape &dims,
+                                    const std::vector<int64_t> (&g)[3]) {
+  std::vector<FusedOp> out;
+  for (const Chained &c : chain) {
+    if ((int)out.size() == kMaxEpi || c.other->dtype != kF32 || c.other->shape != dims || !c.other->buf) break;
+    FusedOp op;
+    if (!flat_stride(c.other, g[0], &op.s0) || !flat_stride(c.other, g[1], &op.s1) ||
+        !flat_stride(c.other, g[2], &op.s2))
+      break;
+    op.arr = c.other;
+    op.code = c.code;
+    op.rev = c.rev;
+    out.push_back(op);
+  }
+  return out;
+}
+
+// dot_general's dimension numbers: false when the lowering would refuse them.
+bool dot_dims(const Op &o, std::vector<int64_t> *lb, std::vector<int64_t> *rb, std::vector<int64_t> *lc,
+              std::vector<int64_t> *rc) {
+  const std::string dn = attr_or(o, "dot_dimension_numbers", "");
+  *lb = ints(field(dn, "lhs_batching_dimensions"));
+  *rb = ints(field(dn, "rhs_batching_dimensions"));
+  *lc = ints(field(dn, "lhs_contracting_dimensions"));
+  *rc = ints(field(dn, "rhs_contracting_dimensions"));
+  if (o.in_tys.size() != 2 || o.out_tys.size() != 1) return false;
+  return lc->size() == 1 && rc->size() == 1 && lb->size() == rb->size();
+}
+
+ArrayP dot_general(const Faults &f, const Op &o, const ArrayP &a, const ArrayP &b,
+                   const std::vector<Chained> &chain = {}) {  // Lower.lean:157-182
   const std::string dn = attr_or(o, "dot_dimension_numbers", "");
   const auto lb = ints(field(dn, "lhs_batching_dimensions"));
   const auto rb = ints(field(dn, "rhs_batching_dimensions"));
@@ -235,12 +283,17 @@ ArrayP dot_general(const Faults &f, const Op &o, const ArrayP &a, const ArrayP &
     pb.push_back(rc[0]);
     ArrayP a3 = reshape(transpose(a, pa), Shape{B, N, K});
     ArrayP b3 = transpose(reshape(transpose(b, pb), Shape{B, M, K}), {0, 2, 1});
-    return reshape(matmul_builtin(a3, b3), out.dims);
+    return apply_chain(reshape(matmul_builtin(a3, b3), out.dims), chain, 0);
   }
   DotOperand L = dot_operand(a, lb, lf, lc[0]);
   DotOperand R = dot_operand(b, rb, rf, rc[0]);
-  ArrayP y = dot_ggml(L, R, B, N, M, K, f.dot_plain ? (int)kTailPlain : default_dot_tail());
-  return reshape(y, out.dims);
+  // Output dims: the batch dims, lhs free dims, rhs free dims (index b, n, m).
+  std::vector<int64_t> g[3];
+  const size_t nb = lb.size(), nl = lf.size();
+  for (size_t d = 0; d < out.dims.size(); d++) g[d < nb ? 0 : d < nb + nl ? 1 : 2].push_back((int64_t)d);
+  const std::vector<FusedOp> epi = fusable_prefix(chain, out.dims, g);
+  ArrayP y = dot_ggml(L, R, B, N, M, K, f.dot_plain ? (int)kTailPlain : default_dot_tail(), epi);
+  return apply_chain(reshape(y, out.dims), chain, epi.size());
 }
 
 // ---- op codes --------------------------------------------------------------------------
@@ -515,6 +568,98 @@ struct Lowerer {
     return run_func_(*fn, args);
   }
 
+  // ---- fusion of element-wise chains into their producer (the mx::compile
+  // role): a dot_general whose result's one use is an f32 add / subtract /
+  // multiply / divide / maximum / minimum of the same shape, whose result's
+  // one use is the next such op, and so on, runs as one kernel that applies
+  // the chain to each output before storing it.  Each op is one IEEE rounding
+  // of the same operands, so the bits are those of the separate ops.
+
+  struct Fusion {
+    std::vector<char> skip;               // the producer and the chain's inner ops
+    std::vector<int> producer;            // at a chain's last op: its producer's index
+    std::vector<std::vector<int>> chain;  // at a producer: its chain's op indices
+  };
+
+  static void count_uses(const Block &b, std::unordered_map<std::string, int> *uses) {
+    for (const Op &o : b.ops) {
+      for (auto &n : o.operands) (*uses)[n]++;
+      for (const Block &r : o.regions) count_uses(r, uses);
+    }
+    for (auto &r : b.ret) (*uses)[r]++;
+  }
+
+  // Whether `e` can take the value `cur` of type `vt` into a fused chain;
+  // *other = the index of its other operand.
+  bool chainable(const Op &e, const Ty &vt, const std::string &cur, int *other) const {
+    if (f.binary_half) return false;  // planted: binary ops through f16
+    uint32_t c = 0;
+    const bool div = e.name == "stablehlo.divide" && !f.divide_builtin;
+    if (!div && !(binary_code(e.name, &c) && (c == kAdd || c == kSub || c == kMul || c == kMax || c == kMin)))
+      return false;
+    if (e.operands.size() != 2 || e.results.size() != 1 || e.in_tys.size() != 2 || e.out_tys.size() != 1 ||
+        !e.regions.empty())
+      return false;
+    for (const Ty *t : {&e.in_tys[0], &e.in_tys[1], &e.out_tys[0]})
+      if (t->el != "f32" || t->dims != vt.dims) return false;
+    const bool l = e.operands[0] == cur, r = e.operands[1] == cur;
+    if (l == r) return false;
+    *other = l ? 1 : 0;
+    return true;
+  }
+
+  Fusion plan_fusion(const Block &b) const {
+    const size_t n = b.ops.size();
+    Fusion fu{std::vector<char>(n, 0), std::vector<int>(n, -1), std::vector<std::vector<int>>(n)};
+    if (f.dot_builtin) return fu;
+    std::unordered_map<std::string, int> uses, user;
+    count_uses(b, &uses);
+    for (size_t k = 0; k < n; k++)
+      for (auto &nm : b.ops[k].operands) user[nm] = (int)k;
+    std::vector<char> claimed(n, 0);
+    for (size_t i = 0; i < n; i++) {
+      const Op &o = b.ops[i];
+      std::vector<int64_t> lb, rb, lc, rc;
+      if (o.name != "stablehlo.dot_general" || o.results.size() != 1 || !dot_dims(o, &lb, &rb, &lc, &rc) ||
+          o.out_tys[0].el != "f32")
+        continue;
+      const Ty &vt = o.out_tys[0];
+      std::string cur = o.results[0];
+      std::vector<int> ch;
+      while ((int)ch.size() < kMaxEpi && uses[cur] == 1) {
+        auto it = user.find(cur);
+        int other = 0;
+        if (it == user.end() || it->second <= (ch.empty() ? (int)i : ch.back()) || claimed[it->second] ||
+            !chainable(b.ops[it->second], vt, cur, &other))
+          break;
+        ch.push_back(it->second);
+        cur = b.ops[it->second].results[0];
+      }
+      if (ch.empty()) continue;
+      fu.skip[i] = 1;
+      for (size_t k = 0; k + 1 < ch.size(); k++) fu.skip[ch[k]] = 1;
+      for (int k : ch) claimed[k] = 1;
+      fu.producer[ch.back()] = (int)i;
+      fu.chain[i] = ch;
+    }
+    return fu;
+  }
+
+  std::vector<ArrayP> run_fused(const Env &env, const std::vector<Op> &ops, int p, const std::vector<int> &ch) {
+    const Op &d = ops[p];
+    std::string cur = d.results[0];
+    std::vector<Chained> chain;
+    for (int k : ch) {
+      const Op &e = ops[k];
+      const bool rev = e.operands[1] == cur;
+      uint32_t c = kDiv;
+      if (e.name != "stablehlo.divide") binary_code(e.name, &c);
+      chain.push_back(Chained{c, rev, get(env, e.operands[rev ? 0 : 1])});
+      cur = e.results[0];
+    }
+    return {dot_general(f, d, get(env, d.operands.at(0)), get(env, d.operands.at(1)), chain)};
+  }
+
   // Run a block whose arguments are `args`, seeing the enclosing env (Lower.lean:503-519).
   std::pair<std::vector<ArrayP>, std::vector<std::pair<bool, int64_t>>> run_region(
       const Env &env0, const Known &known0, const Block &b, const std::vector<ArrayP> &args,
@@ -526,11 +671,15 @@ struct Lowerer {
       if (i < argk.size() && argk[i].first) known[b.args[i].first] = argk[i].second;
       else known.erase(b.args[i].first);
     }
-    for (const Op &o : b.ops) {
-      auto rs = run_op(env, known, o);
+    const Fusion fu = plan_fusion(b);
+    for (size_t i = 0; i < b.ops.size(); i++) {
+      const Op &o = b.ops[i];
+      if (fu.skip[i]) continue;  // a fused producer or inner chain op: runs with the chain's last op
+      auto rs = fu.producer[i] >= 0 ? run_fused(env, b.ops, fu.producer[i], fu.chain[fu.producer[i]])
+                                    : run_op(env, known, o);
       if (rs.size() != o.results.size())
         fail(strf("%s: %zu results for %zu names", o.name.c_str(), rs.size(), o.results.size()));
-      for (size_t i = 0; i < rs.size(); i++) env[o.results[i]] = rs[i];
+      for (size_t j = 0; j < rs.size(); j++) env[o.results[j]] = rs[j];
       if (o.results.size() == 1) {
         int64_t v;
         if (const_eval(known, o, &v)) known[o.results[0]] = v;

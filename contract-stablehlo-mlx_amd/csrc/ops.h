@@ -72,11 +72,23 @@ struct DotOperand {
   int64_t sb = 0, sf = 0, sk = 0;
 };
 
+// One element-wise binary32 op fused into a producer's store: v = op(v, o)
+// (op(o, v) when `rev`), o the element of `arr` at i0*s0 + i1*s1 + i2*s2 for
+// the producer's output index (i0, i1, i2).  Same bits as the separate op.
+constexpr int kMaxEpi = 4;  // fused ops per producer
+struct FusedOp {
+  ArrayP arr;  // f32; keeps the buffer alive
+  int64_t s0 = 0, s1 = 0, s2 = 0;
+  uint32_t code = 0;  // kAdd, kSub, kMul, kDiv, kMax, kMin
+  bool rev = false;
+};
+
 // y[(b*N + n)*M + m] = dot over k of lhs(b, n, k) and rhs(b, m, k), each
 // output in ggml_vec_dot_f32's order (16 FMA accumulators over blocks of 16,
-// GGML_F32x4_REDUCE, vaddvq_f32, then the tail).  Output shape [B*N*M].
+// GGML_F32x4_REDUCE, vaddvq_f32, then the tail), then the fused ops `epi` at
+// index (b, n, m) in order (at most 4).  Output shape [B*N*M].
 ArrayP dot_ggml(const DotOperand &lhs, const DotOperand &rhs, int64_t B, int64_t N, int64_t M,
-                int64_t K, int tail);
+                int64_t K, int tail, const std::vector<FusedOp> &epi = {});
 
 // The reference's Run.mulMat surface (Run.lean:155-158): w rows of K, x rows
 // of K; y[r*M + m] = dot(w row (r/N)*wBatchStride/K + m, x row r).

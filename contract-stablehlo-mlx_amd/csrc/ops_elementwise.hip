@@ -7,6 +7,7 @@
 
 #include <cmath>
 
+#include "epilogue.h"
 #include "ops.h"
 
 namespace shlo {
@@ -346,7 +347,11 @@ template <class T>
 struct BinaryF {
   uint32_t op;
   __device__ T operator()(T a, T b) const {
-    if constexpr (is_flt<T>()) {
+    if constexpr (std::is_same<T, float>::value) {  // shared with the fused epilogues
+      if (op == kDivApprox) return a * __builtin_amdgcn_rcpf(b);
+      if (op == kRem) return std::fmod(a, b);
+      return f32_binary(op, a, b);
+    } else if constexpr (is_flt<T>()) {
       using C = typename std::conditional<std::is_same<T, double>::value, double, T>::type;
       const C x = (C)a, y = (C)b;
       switch (op) {

@@ -1,0 +1,267 @@
+"""GPU parity of element-wise chains fused into dot_general's store.
+
+A dot_general whose result flows only through f32 add / subtract / multiply
+/ divide / maximum / minimum ops of its shape runs as one kernel that applies
+them to each output before storing it.  Each case here runs such a chain,
+eager and hipGraph-compiled, against the oracle's dot followed by the same
+IEEE operations in numpy (one rounding each, in the same operand order), and
+covers the cases the fusion must decline or cut short: more than four ops, an
+operand whose strides do not flatten over the output's (batch, row, column)
+groups, intermediate values with other uses, and planted faults."""
+import numpy as np
+import pytest
+
+pytestmark = [pytest.mark.gpu, pytest.mark.usefixtures("graph_mode")]
+
+F32 = np.float32
+
+
+def t(shape):
+    return "tensor<" + "".join(f"{d}x" for d in shape) + "f32>"
+
+
+def same_bits(a, b):
+    return a.shape == b.shape and np.array_equal(np.ascontiguousarray(a).view(np.uint32),
+                                                 np.ascontiguousarray(b).view(np.uint32))
+
+
+def np_binary(op, x, y):
+    """The binary32 semantics of the op table (one IEEE rounding; maximum and
+    minimum propagate NaN as x + y and order -0 below +0)."""
+    x, y = np.asarray(x, F32), np.asarray(y, F32)
+    with np.errstate(all="ignore"):
+        if op == "add":
+            return (x + y).astype(F32)
+        if op == "subtract":
+            return (x - y).astype(F32)
+        if op == "multiply":
+            return (x * y).astype(F32)
+        if op == "divide":
+            return (x / y).astype(F32)
+        nan = np.isnan(x) | np.isnan(y)
+        eq = x == y
+        if op == "maximum":
+            pick = np.where(eq, np.where(np.signbit(x), y, x), np.where(x > y, x, y))
+        else:
+            pick = np.where(eq, np.where(np.signbit(x), x, y), np.where(x < y, x, y))
+        return np.where(nan, x + y, pick).astype(F32)
+
+
+class Chain:
+    """dot_general of [*batch, N, K] x [*batch, K, M] (or its transposed
+    contraction), then ops [(name, arg, how, rev)]: arg is an extra function
+    argument; how = None (already the output shape), ("bcast", dims) for a
+    broadcast_in_dim, or ("perm", perm) for a transpose; rev puts the running
+    value on the right."""
+
+    def __init__(self, batch, N, K, M, ops, rhs_mk=False, extra_returns=()):
+        self.batch, self.N, self.K, self.M, self.ops = tuple(batch), N, K, M, ops
+        self.rhs_mk, self.extra = rhs_mk, extra_returns
+
+    @property
+    def out_shape(self):
+        return self.batch + (self.N, self.M)
+
+    def module(self):
+        nb = len(self.batch)
+        a_sh = self.batch + (self.N, self.K)
+        b_sh = self.batch + ((self.M, self.K) if self.rhs_mk else (self.K, self.M))
+        o = self.out_shape
+        bd = list(range(nb))
+        dn = (f"#stablehlo.dot<lhs_batching_dimensions = {bd}, rhs_batching_dimensions = {bd}, "
+              f"lhs_contracting_dimensions = [{nb + 1}], rhs_contracting_dimensions = "
+              f"[{nb + 1 if self.rhs_mk else nb}]>")
+        args = [f"%a: {t(a_sh)}", f"%b: {t(b_sh)}"]
+        lines = [f'    %v0 = "stablehlo.dot_general"(%a, %b) {{dot_dimension_numbers = {dn}}} : '
+                 f"({t(a_sh)}, {t(b_sh)}) -> {t(o)}\n"]
+        cur = "%v0"
+        names = ["%v0"]
+        for i, (name, arg, how, rev) in enumerate(self.ops):
+            args.append(f"%x{i}: {t(arg.shape)}")
+            other = f"%x{i}"
+            if how is not None and how[0] == "bcast":
+                dims = ", ".join(str(d) for d in how[1])
+                lines.append(f'    %b{i} = "stablehlo.broadcast_in_dim"(%x{i}) {{broadcast_dimensions = '
+                             f"array<i64{': ' + dims if dims else ''}>}} : ({t(arg.shape)}) -> {t(o)}\n")
+                other = f"%b{i}"
+            elif how is not None and how[0] == "perm":
+                perm = ", ".join(str(d) for d in how[1])
+                lines.append(f'    %b{i} = "stablehlo.transpose"(%x{i}) {{permutation = array<i64: {perm}>}} : '
+                             f"({t(arg.shape)}) -> {t(o)}\n")
+                other = f"%b{i}"
+            l, r = (other, cur) if rev else (cur, other)
+            lines.append(f'    %v{i + 1} = "stablehlo.{name}"({l}, {r}) : ({t(o)}, {t(o)}) -> {t(o)}\n')
+            cur = f"%v{i + 1}"
+            names.append(cur)
+        rets = [cur] + [names[k] for k in self.extra]
+        sig = ", ".join(t(o) for _ in rets)
+        return (f"module {{\n  func.func public @main({', '.join(args)}) -> ({sig}) {{\n" + "".join(lines) +
+                f"    func.return {', '.join(rets)} : {sig}\n  }}\n}}\n")
+
+    def expect(self, oracle, a, b, tail):
+        B = int(np.prod(self.batch)) if self.batch else 1
+        lhs = a.reshape(B, self.N, self.K)
+        rhs = b.reshape(B, self.M, self.K) if self.rhs_mk else \
+            np.ascontiguousarray(b.reshape(B, self.K, self.M).transpose(0, 2, 1))
+        v = oracle.dot_general_bnk(np.ascontiguousarray(lhs), np.ascontiguousarray(rhs), tail)
+        v = v.reshape(self.out_shape)
+        vals = [v]
+        o = self.out_shape
+        for name, arg, how, rev in self.ops:
+            if how is None:
+                other = arg
+            elif how[0] == "bcast":
+                shp = [1] * len(o)
+                for k, d in enumerate(how[1]):
+                    shp[d] = arg.shape[k]
+                other = np.broadcast_to(arg.reshape(shp), o)
+            else:
+                other = arg.transpose(how[1])
+            v = np_binary(name, other, v) if rev else np_binary(name, v, other)
+            vals.append(v)
+        return [v] + [vals[k] for k in self.extra]
+
+
+def run(text, inputs, faults=0, compile=True):
+    import shlo_hip
+    f = shlo_hip.Module(text).prepare(faults, compile)
+    return [o.numpy() for o in f.call([shlo_hip.from_numpy(np.ascontiguousarray(x)) for x in inputs])]
+
+
+def normal(oracle, seed, shape, sigma=1.0):
+    x, _ = oracle.fill_normal(seed, sigma, int(np.prod(shape)))
+    return x.reshape(shape)
+
+
+def check(oracle, ch, seed=5, flavors=(0, 1)):
+    import shlo_hip
+    a_sh = ch.batch + (ch.N, ch.K)
+    b_sh = ch.batch + ((ch.M, ch.K) if ch.rhs_mk else (ch.K, ch.M))
+    a, b = normal(oracle, seed, a_sh), normal(oracle, seed + 1, b_sh)
+    ins = [a, b] + [arg for _, arg, _, _ in ch.ops]
+    text = ch.module()
+    for flavor in flavors:
+        want = ch.expect(oracle, a, b, flavor)
+        shlo_hip.set_flavor(flavor)
+        try:
+            for compile in (True, False):
+                got = run(text, ins, compile=compile)
+                assert len(got) == len(want)
+                for g, w in zip(got, want):
+                    assert same_bits(g, w), (flavor, compile)
+        finally:
+            shlo_hip.set_flavor(0)
+    return text, ins
+
+
+def scalar(v):
+    return np.array(v, F32)
+
+
+@pytest.mark.parametrize("S,K", [(70, 64), (128, 64), (96, 33)])
+def test_attention_scale_and_mask(oracle, S, K):
+    """Q K^T [2,3,S,S] (contraction over both operands' last dim), times a
+    broadcast scalar, plus a broadcast causal mask [S,S] over dims 2, 3."""
+    mask = np.where(np.triu(np.ones((S, S), bool), 1), F32(-np.inf), F32(0))
+    ch = Chain((2, 3), S, K, S, [("multiply", scalar(0.125), ("bcast", ()), False),
+                                 ("add", mask, ("bcast", (2, 3)), False)], rhs_mk=True)
+    check(oracle, ch)
+
+
+@pytest.mark.parametrize("N,K,M", [(256, 64, 192), (130, 512, 70), (64, 1024, 128), (33, 17, 9)])
+def test_bias_and_residual(oracle, N, K, M):
+    """x W + bias (broadcast over rows), then a residual on the left (rev):
+    the persistent kernel (K <= 512), the per-tile kernel, partial tiles and
+    row tails."""
+    bias = normal(oracle, 9, (M,), 0.5)
+    res = normal(oracle, 10, (N, M))
+    ch = Chain((), N, K, M, [("add", bias, ("bcast", (1,)), False), ("add", res, None, True)])
+    check(oracle, ch)
+
+
+@pytest.mark.parametrize("name", ["subtract", "divide", "maximum", "minimum"])
+@pytest.mark.parametrize("rev", [False, True])
+def test_each_op_both_orders(oracle, name, rev):
+    """Each fusable op with the dot's value on either side; the other operand
+    holds zeros of both signs, infinities, NaN, subnormals and values equal to
+    the dot's outputs."""
+    N, K, M = 96, 48, 80
+    other = normal(oracle, 12, (N, M))
+    flat = other.reshape(-1)
+    flat[::7] = 0.0
+    flat[1::7] = -0.0
+    flat[2::11] = np.inf
+    flat[3::11] = -np.inf
+    flat[4::13] = np.nan
+    flat[5::13] = np.float32(1e-40)
+    a, b = normal(oracle, 5, (N, K)), normal(oracle, 6, (K, M))
+    v = oracle.dot_general_bnk(a[None], np.ascontiguousarray(b.T)[None], 0)[0]
+    flat[6::17] = v.reshape(-1)[6::17]  # equal operands (maximum / minimum pick by sign)
+    ch = Chain((), N, K, M, [(name, other, None, rev)])
+    check(oracle, ch, flavors=(0,))
+
+
+def test_longer_chain_than_fused(oracle):
+    """Six ops: the first four fuse, the rest run as separate kernels."""
+    N, K, M = 128, 64, 128
+    ops = [("add", normal(oracle, 20, (M,)), ("bcast", (1,)), False),
+           ("multiply", scalar(1.5), ("bcast", ()), False),
+           ("subtract", normal(oracle, 21, (N, M)), None, True),
+           ("maximum", normal(oracle, 22, (N,)), ("bcast", (0,)), False),
+           ("divide", normal(oracle, 23, (N, M)), None, False),
+           ("minimum", scalar(0.75), ("bcast", ()), True)]
+    check(oracle, Chain((), N, K, M, ops))
+
+
+def test_operand_strides_that_do_not_flatten(oracle):
+    """An operand transposed across the two batch dims has no single batch
+    stride: the chain stops there and the op runs on its own."""
+    B1, B2, N, K, M = 3, 2, 64, 32, 64
+    tr = normal(oracle, 30, (B2, B1, N, M))
+    ops = [("add", normal(oracle, 31, (M,)), ("bcast", (3,)), False),
+           ("add", tr, ("perm", (1, 0, 2, 3)), False),
+           ("multiply", normal(oracle, 32, (B1, B2, N, M)), None, True)]
+    check(oracle, Chain((B1, B2), N, K, M, ops))
+
+
+def test_transposed_operand_flattens(oracle):
+    """A transposed [M,N] operand over an [N,M] output has strides (1, N): one
+    dim per group, so it fuses."""
+    N, K, M = 96, 64, 160
+    ch = Chain((), N, K, M, [("add", normal(oracle, 32, (M, N)), ("perm", (1, 0)), False)])
+    check(oracle, ch)
+
+
+def test_intermediate_with_another_use(oracle):
+    """The first op's result is also returned: the chain ends there."""
+    N, K, M = 64, 64, 64
+    ops = [("add", normal(oracle, 40, (N, M)), None, False), ("multiply", normal(oracle, 41, (N, M)), None, False)]
+    check(oracle, Chain((), N, K, M, ops, extra_returns=(1,)))
+
+
+def test_dot_result_with_two_uses(oracle):
+    """The dot's own value is returned too: nothing fuses."""
+    N, K, M = 64, 32, 64
+    ops = [("add", normal(oracle, 42, (N, M)), None, False)]
+    check(oracle, Chain((), N, K, M, ops, extra_returns=(0,)))
+
+
+def test_many_batches_simple_kernel(oracle):
+    """More than 65535 batches take the one-thread-per-output kernel, which
+    applies the same chain."""
+    B, N, K, M = 70000, 1, 20, 2
+    ops = [("add", normal(oracle, 43, (M,)), ("bcast", (2,)), False),
+           ("multiply", normal(oracle, 44, (B,)), ("bcast", (0,)), True)]
+    check(oracle, Chain((B,), N, K, M, ops), flavors=(1,))
+
+
+def test_planted_faults_still_differ(oracle):
+    import shlo_hip
+    N, K, M = 64, 64, 64
+    ch = Chain((), N, K, M, [("add", normal(oracle, 50, (M,)), ("bcast", (1,)), False),
+                             ("divide", normal(oracle, 51, (N, M)), None, False)])
+    text, ins = check(oracle, ch, flavors=(0,))
+    want = ch.expect(oracle, ins[0], ins[1], 0)[0]
+    for fault in ("dot_plain", "dot_builtin", "binary_half", "divide_builtin", "broadcast_first"):
+        got = run(text, ins, faults=shlo_hip.fault_bits(fault))[0]
+        assert not same_bits(got, want), fault
