@@ -64,36 +64,62 @@ __device__ __forceinline__ float epi_apply(const Epilogue &e, float v, int64_t i
   return v;
 }
 
-// The fused ops on the 8 outputs a lane of the matrix kernels finishes: rows
-// n + 8 (r / 4) + r % 4 (r = 0..7, each clamped to nmax so a discarded row
-// reads in range) of column m in batch b.  One uniform switch per op, then the
-// op on all 8 values.
-template <uint32_t C>
-__device__ __forceinline__ void epi_op8(float (&v)[8], const float (&w)[8], uint32_t rev) {
+// The fused ops on NV output values a lane holds: value r sits at element
+// offset off(op, r) of each op's operand (a producer clamps the offsets of
+// values it discards into range).  One uniform switch per op, then the op on
+// all NV values, their operand loads issued together.
+template <uint32_t C, int NV>
+__device__ __forceinline__ void epi_op(float (&v)[NV], const float (&w)[NV], uint32_t rev) {
 #pragma unroll
-  for (int r = 0; r < 8; r++) v[r] = rev ? f32_binary(C, w[r], v[r]) : f32_binary(C, v[r], w[r]);
+  for (int r = 0; r < NV; r++) v[r] = rev ? f32_binary(C, w[r], v[r]) : f32_binary(C, v[r], w[r]);
 }
 
-__device__ __forceinline__ void epi_rows8(const Epilogue &e, float (&v)[8], int64_t b, int64_t n, int64_t nmax,
-                                          int64_t m) {
+// The same in two steps, for a producer that can issue the operand loads
+// long before its values are ready: epi_load_n, then epi_ops_n.
+template <int NV, class Off>
+__device__ __forceinline__ void epi_load_n(const Epilogue &e, float (&w)[kMaxEpi][NV], Off off) {
+#pragma unroll
+  for (int k = 0; k < kMaxEpi; k++) {
+    if (k >= e.n) break;
+#pragma unroll
+    for (int r = 0; r < NV; r++) w[k][r] = e.op[k].p[off(e.op[k], r)];
+  }
+}
+
+template <int NV>
+__device__ __forceinline__ void epi_ops_n(const Epilogue &e, float (&v)[NV], const float (&w)[kMaxEpi][NV]) {
 #pragma unroll
   for (int k = 0; k < kMaxEpi; k++) {
     if (k >= e.n) break;
     const EpiOp &o = e.op[k];
-    const float *p = o.p + b * o.s0 + m * o.s2;
-    float w[8];
-#pragma unroll
-    for (int r = 0; r < 8; r++) {
-      const int64_t nr = n + 8 * (r / 4) + r % 4;
-      w[r] = p[(nr < nmax ? nr : nmax) * o.s1];
-    }
     switch (o.code) {
-      case kAdd: epi_op8<kAdd>(v, w, o.rev); break;
-      case kSub: epi_op8<kSub>(v, w, o.rev); break;
-      case kMul: epi_op8<kMul>(v, w, o.rev); break;
-      case kDiv: epi_op8<kDiv>(v, w, o.rev); break;
-      case kMax: epi_op8<kMax>(v, w, o.rev); break;
-      case kMin: epi_op8<kMin>(v, w, o.rev); break;
+      case kAdd: epi_op<kAdd>(v, w[k], o.rev); break;
+      case kSub: epi_op<kSub>(v, w[k], o.rev); break;
+      case kMul: epi_op<kMul>(v, w[k], o.rev); break;
+      case kDiv: epi_op<kDiv>(v, w[k], o.rev); break;
+      case kMax: epi_op<kMax>(v, w[k], o.rev); break;
+      case kMin: epi_op<kMin>(v, w[k], o.rev); break;
+      default: break;
+    }
+  }
+}
+
+template <int NV, class Off>
+__device__ __forceinline__ void epi_apply_n(const Epilogue &e, float (&v)[NV], Off off) {
+#pragma unroll
+  for (int k = 0; k < kMaxEpi; k++) {
+    if (k >= e.n) break;
+    const EpiOp &o = e.op[k];
+    float w[NV];
+#pragma unroll
+    for (int r = 0; r < NV; r++) w[r] = o.p[off(o, r)];
+    switch (o.code) {
+      case kAdd: epi_op<kAdd>(v, w, o.rev); break;
+      case kSub: epi_op<kSub>(v, w, o.rev); break;
+      case kMul: epi_op<kMul>(v, w, o.rev); break;
+      case kDiv: epi_op<kDiv>(v, w, o.rev); break;
+      case kMax: epi_op<kMax>(v, w, o.rev); break;
+      case kMin: epi_op<kMin>(v, w, o.rev); break;
       default: break;
     }
   }

@@ -376,7 +376,13 @@ __device__ __forceinline__ void dot_store_rows(const MfmaOperand &X, const MfmaO
       v[r] = sumf;
     }
   }
-  if (ep.n > 0) epi_rows8(ep, v, b, n, N - 1, m < M ? m : M - 1);
+  if (ep.n > 0) {
+    const int64_t mc = m < M ? m : M - 1;
+    epi_apply_n(ep, v, [&](const EpiOp &o, int r) {
+      const int64_t nr = n + 8 * (r / 4) + r % 4;
+      return b * o.s0 + (nr < N ? nr : N - 1) * o.s1 + mc * o.s2;
+    });
+  }
   float *y = Y + (b * N + n) * M + m;
   if (whole) {
 #pragma unroll
@@ -670,14 +676,15 @@ constexpr int64_t kPersistStages = 4;
 // most, so t <= (1 - 2^-20) 2^53 u implies an exact total below 2^53 u, and
 // then t is that total.
 //
-// softmax_inv first tests the whole row at once (a wave's tree sum T).  A row
-// that fails (parts spread over more than about 2^50, a NaN, an infinity)
-// still needs only inv = (float)(1.0 / S) of the in-order sum S, and
-// f(x) = (float)(1.0 / x) is non-increasing in x.  For n <= 2^11 non-negative
-// terms S lies within a relative (n-1) 2^-53 < 2^-42 of the exact total and T
-// within 2^-48 of it, so S lies in [T (1 - 2^-41), T (1 + 2^-41)], inside
+// ordered_sum_apply first tests the whole row at once (a wave's tree sum T).
+// A row that fails (parts spread over more than about 2^50, a NaN, an
+// infinity) still needs only a monotone f(S) of the in-order sum S: softmax's
+// inv = (float)(1.0 / S), non-increasing, or norm's variance
+// (float)(S / cols), non-decreasing.  For n <= 2^11 non-negative terms S lies
+// within a relative (n-1) 2^-53 < 2^-42 of the exact total and T within 2^-48
+// of it, so S lies in [T (1 - 2^-41), T (1 + 2^-41)], inside
 // [lo, hi] = T (1 -+ 2^-40) computed in binary64; f(lo) == f(hi) then fixes
-// f(S).  Only a row whose 1/S falls within about 2^-40 of a binary32 rounding
+// f(S).  Only a row whose f(S) falls within about 2^-40 of a binary32 rounding
 // boundary fails that as well (about one row in 10^5 of those); it walks its
 // parts in segments of 16 consecutive groups (one 16-lane row of the wave,
 // reduced with DPP), adding a segment's tree sum in one step when the exactness
@@ -697,6 +704,18 @@ __device__ __forceinline__ int part_ulp_exp(float p) {
 // field e + 925, the top 19 fraction bits set.
 __device__ __forceinline__ double exact_limit(int e) {
   return __builtin_bit_cast(double, ((uint64_t)(e + 925) << 52) | (((1ull << 19) - 1) << 33));
+}
+
+// The biased exponent e (in part_ulp_exp's units: the bit is 2^(e-150)) of the
+// lowest set bit of a binary64 s, 255 for 0: every partial sum that s and
+// multiples of that bit make is a multiple of it.
+__device__ __forceinline__ int low_bit_exp(double s) {
+  const uint64_t b = __builtin_bit_cast(uint64_t, s) & 0x7FFFFFFFFFFFFFFFull;
+  if (b == 0) return 255;
+  const int E = (int)(b >> 52);
+  const uint64_t m = b & ((1ull << 52) - 1);
+  const uint64_t sig = E ? (m | (1ull << 52)) : m;
+  return (E ? E : 1) - 1075 + __builtin_ctzll(sig) + 150;
 }
 
 // DPP within 16-lane rows: quad_perm [1,0,3,2], quad_perm [2,3,0,1],
@@ -733,22 +752,13 @@ __device__ __forceinline__ double lane_d(double v, int l) {
   return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
 }
 
-// inv = (float)(1.0 / S) for the row whose group part g = l + 64 j lane l
-// holds as part[j] (+0 for g >= G), followed by tail values on lanes < T.
-// The result is the same on every lane.
-template <int J, bool FULL>
-__device__ __forceinline__ float softmax_inv(const float (&part)[J], int G, float tail, int T, int float_sum) {
+// fin(S) for the in-order binary64 sum S of a row's parts: group part
+// g = l + 64 j, held by lane l as part[j] (+0 for g >= G), then tail values
+// on lanes < T.  fin must be monotone (either way) on binary64 values; the
+// result is the same on every lane.
+template <int J, bool FULL, class Fin>
+__device__ __forceinline__ float ordered_sum_apply(const float (&part)[J], int G, float tail, int T, Fin fin) {
   const int lane = threadIdx.x % kWave;
-  if (float_sum) {  // planted: the denominator summed in binary32 (Shaders.lean:120-122)
-    float fs = 0.0f;
-#pragma unroll
-    for (int j = 0; j < J; j++) {
-      const int n = FULL ? kWave : min(kWave, G - kWave * j);
-      for (int l = 0; l < n; l++) fs = fs + lane_f(part[j], l);
-    }
-    for (int l = 0; l < T; l++) fs = fs + lane_f(tail, l);
-    return 1.0f / fs;
-  }
   double ls = 0.0;
   int le = 255;
 #pragma unroll
@@ -765,10 +775,10 @@ __device__ __forceinline__ float softmax_inv(const float (&part)[J], int G, floa
     ls = ls + __shfl_xor(ls, o, kWave);
     le = min(le, __shfl_xor(le, o, kWave));
   }
-  if (ls <= exact_limit(le)) return (float)(1.0 / ls);
+  if (ls <= exact_limit(le)) return fin(ls);
   const double d = ls * 0x1p-40;  // exact: ls >= 2^-149 or ls = 0
-  const float inv_lo = (float)(1.0 / (ls + d)), inv_hi = (float)(1.0 / (ls - d));
-  if (inv_lo == inv_hi) return inv_lo;  // false for NaN and infinity
+  const float f_lo = fin(ls - d), f_hi = fin(ls + d);
+  if (f_lo == f_hi) return f_lo;  // false for NaN and infinity
   // In order, segment by segment: segment q = 4 j + r holds groups
   // 64 j + 16 r .. 64 j + 16 r + 15 (lanes 16 r .. 16 r + 15 of slice j).
   double s = 0.0;
@@ -795,7 +805,23 @@ __device__ __forceinline__ float softmax_inv(const float (&part)[J], int G, floa
     }
   }
   for (int l = 0; l < T; l++) s = s + (double)lane_f(tail, l);
-  return (float)(1.0 / s);
+  return fin(s);
+}
+
+// softmax's inv = (float)(1.0 / S), S as in ordered_sum_apply.
+template <int J, bool FULL>
+__device__ __forceinline__ float softmax_inv(const float (&part)[J], int G, float tail, int T, int float_sum) {
+  if (float_sum) {  // planted: the denominator summed in binary32 (Shaders.lean:120-122)
+    float fs = 0.0f;
+#pragma unroll
+    for (int j = 0; j < J; j++) {
+      const int n = FULL ? kWave : min(kWave, G - kWave * j);
+      for (int l = 0; l < n; l++) fs = fs + lane_f(part[j], l);
+    }
+    for (int l = 0; l < T; l++) fs = fs + lane_f(tail, l);
+    return 1.0f / fs;
+  }
+  return ordered_sum_apply<J, FULL>(part, G, tail, T, [](double x) { return (float)(1.0 / x); });
 }
 
 // ggml soft_max, one wave per row.  Lane l owns the four-element groups
@@ -956,68 +982,197 @@ int env_int(const char *name, int dflt) {
 
 // ---- norm ---------------------------------------------------------------------------
 
-// One wave per row, the row staged in LDS.  ggml_vec_sum_f32 without
-// Accelerate (a binary64 sum in element order), mean = (float)sum / (float)N,
-// ggml_vec_cvar_f32 (binary64 sum of four-lane groups, then the scalar tail),
-// var = (float)(s2 / N), scale = 1/sqrtf(var + eps), y = (x - mean)*scale
-// (Shaders.lean:147-166).  The sequential sums run on lane 0.
-__global__ void __launch_bounds__(256) norm_k(int64_t rows, int cols, float eps, int gpu_ops,
-                                              const float *__restrict__ X, float *__restrict__ Y) {
+// The planted norm (Shaders.lean:147-166 with binary32 sums and the GPU's own
+// approximate reciprocal and square root): one wave per row, the row staged in
+// LDS, the sequential sums on lane 0.
+__global__ void __launch_bounds__(256) norm_planted_k(int64_t rows, int cols, float eps,
+                                                      const float *__restrict__ X, float *__restrict__ Y) {
   extern __shared__ float lds[];
   const int waves = blockDim.x / kWave;
   const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
-  const int G = cols / 4;
-  float *xr = lds + wave * (cols + 4 + G + 4);
-  float *parts = xr + cols + 4;
+  float *xr = lds + wave * (cols + 4);
   for (int64_t row = blockIdx.x * (int64_t)waves + wave; row < rows; row += (int64_t)gridDim.x * waves) {
     const float *x = X + row * cols;
     float *y = Y + row * cols;
     for (int i = lane; i < cols; i += kWave) xr[i] = x[i];
     wave_sync();
     float mean = 0.0f, scl = 0.0f;
-    if (gpu_ops) {  // planted: binary32 sums and the GPU's own / and sqrt
-      if (lane == 0) {
-        float s = 0.0f;
-        for (int i = 0; i < cols; i++) s = s + xr[i];
-        mean = s / (float)cols;
-        float s2 = 0.0f;
-        for (int i = 0; i < cols; i++) {
-          const float d = xr[i] - mean;
-          s2 = s2 + d * d;
-        }
-        scl = __builtin_amdgcn_rcpf(__builtin_amdgcn_sqrtf(s2 / (float)cols + eps));
+    if (lane == 0) {
+      float s = 0.0f;
+      for (int i = 0; i < cols; i++) s = s + xr[i];
+      mean = s / (float)cols;
+      float s2 = 0.0f;
+      for (int i = 0; i < cols; i++) {
+        const float d = xr[i] - mean;
+        s2 = s2 + d * d;
       }
-    } else {
-      if (lane == 0) {
-        double s = 0.0;
-        for (int i = 0; i < cols; i++) s = s + (double)xr[i];
-        mean = (float)s / (float)cols;
-      }
-      mean = __shfl(mean, 0, kWave);
-      for (int g = lane; g < G; g += kWave) {
-        const float d0 = xr[4 * g] - mean, d1 = xr[4 * g + 1] - mean;
-        const float d2 = xr[4 * g + 2] - mean, d3 = xr[4 * g + 3] - mean;
-        const float q0 = d0 * d0, q1 = d1 * d1, q2 = d2 * d2, q3 = d3 * d3;
-        parts[g] = (q0 + q1) + (q2 + q3);
-      }
-      wave_sync();
-      if (lane == 0) {
-        double s2 = 0.0;
-        for (int g = 0; g < G; g++) s2 = s2 + (double)parts[g];
-        for (int i = 4 * G; i < cols; i++) {
-          const float d = xr[i] - mean;
-          const float q = d * d;
-          s2 = s2 + (double)q;
-        }
-        const float var = (float)(s2 / (double)cols);
-        scl = 1.0f / sqrtf(var + eps);
-      }
+      scl = __builtin_amdgcn_rcpf(__builtin_amdgcn_sqrtf(s2 / (float)cols + eps));
     }
     mean = __shfl(mean, 0, kWave);
     scl = __shfl(scl, 0, kWave);
     for (int i = lane; i < cols; i += kWave) y[i] = (xr[i] - mean) * scl;
     wave_sync();
   }
+}
+
+// ggml norm, one wave per row (rows of at most 4096 columns): lane l holds the
+// four-element groups g = l + 64 j as float4 and, on lanes < cols % 4, one
+// tail element.  Both binary64 sums of Shaders.lean:130-166 are taken in
+// ggml's order only where the order can matter:
+// * The mean's sum of the elements x_i (any signs).  Every x_i is a multiple
+//   of u, the smallest ulp among the nonzero x_i, and every partial sum in any
+//   order is bounded by A = sum |x_i|: if A < 2^53 u, no addition rounds and
+//   the in-order chain equals a tree sum.  A wave computes the tree sum t, the
+//   tree sum a of |x_i| and u, and takes a <= (1 - 2^-20) 2^53 u as the test
+//   (the softmax argument, on |x_i|).  Otherwise the chain lies within
+//   (cols - 1) 2^-53 A of the exact sum (cols - 1 additions, each rounding
+//   by at most 2^-53 of a partial sum bounded by A) and t within
+//   (4 J + 7) 2^-53 A (a lane's serial sum, then six butterfly levels), so
+//   mean = (float)s / cols, monotone in s, is fixed when it agrees at
+//   t -+ a (cols + 4 J + 8) 2^-52, twice that bound.  A row that fails both
+//   (a NaN, an infinity, or a mean within about cols 2^-52 A of a rounding
+//   boundary) adds its elements in order, 64 at a time where no addition in
+//   them can round.
+// * The variance's sum of the group parts (q0 + q1) + (q2 + q3) of
+//   q = (x - mean)^2 and the tail's q, all >= 0: ordered_sum_apply with
+//   f(S) = (float)(S / cols).
+// Then scale = 1 / sqrtf(var + eps) and y = (x - mean) * scale, followed (EPI)
+// by the fused element-wise ops at index (0, row, column).
+template <int J, bool FULL, bool EPI>
+__global__ void __launch_bounds__(256) norm_rows_k(int64_t rows, int cols, float eps, Epilogue ep,
+                                                   const float *__restrict__ X, float *__restrict__ Y) {
+  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  const int G = cols / 4, T = cols - 4 * G;
+  const int64_t row = blockIdx.x * 4LL + wave;
+  if (row >= rows) return;  // the whole wave; no barrier follows
+  const float *x = X + row * cols;
+  float4 e[J];
+#pragma unroll
+  for (int j = 0; j < J; j++) {  // rows start 16-byte aligned only when cols % 4 == 0
+    const int g = lane + kWave * j;
+    const float *p = x + 4 * g;
+    e[j] = (FULL || g < G) ? (T == 0 ? ld4(p) : make_float4(p[0], p[1], p[2], p[3]))
+                           : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  }
+  const float et = lane < T ? x[4 * G + lane] : 0.0f;
+  // The fused ops' operands do not depend on the row's sums: their loads go
+  // out now and land under the reductions.
+  float w[kMaxEpi][4 * J], wt[kMaxEpi][1];
+  if (EPI) {
+    epi_load_n(ep, w, [&](const EpiOp &o, int r) {
+      const int g = lane + kWave * (r / 4);
+      const int c = (FULL || g < G) ? 4 * g + r % 4 : 0;  // a discarded group reads column 0
+      return row * o.s1 + c * o.s2;
+    });
+    if (T > 0) epi_load_n(ep, wt, [&](const EpiOp &o, int) { return row * o.s1 + (lane < T ? 4 * G + lane : 0) * o.s2; });
+  }
+  double ls = 0.0, la = 0.0;
+  int le = 255;
+  auto take = [&](float v) {
+    ls = ls + (double)v;
+    la = la + (double)__builtin_fabsf(v);
+    le = min(le, part_ulp_exp(v));
+  };
+#pragma unroll
+  for (int j = 0; j < J; j++) {  // groups past G hold +0: no effect on any of the three
+    take(e[j].x);
+    take(e[j].y);
+    take(e[j].z);
+    take(e[j].w);
+  }
+  take(et);
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) {
+    ls = ls + __shfl_xor(ls, o, kWave);
+    la = la + __shfl_xor(la, o, kWave);
+    le = min(le, __shfl_xor(le, o, kWave));
+  }
+  const float fc = (float)cols;
+  float mean;
+  if (la <= exact_limit(le)) {
+    mean = (float)ls / fc;
+  } else {
+    const double d = la * ((double)(cols + 4 * J + 8) * 0x1p-52);
+    const float lo = (float)(ls - d) / fc, hi = (float)(ls + d) / fc;
+    if (lo == hi) {  // false for NaN
+      mean = lo;
+    } else {
+      // In order, 64 elements (16 lanes of one slice) at a time: a segment
+      // whose additions to the running sum s cannot round (|s| plus the
+      // segment's sum of |x| below 2^53 times the smaller of s's lowest set
+      // bit and the segment's smallest ulp) is added as its tree sum, any
+      // other element by element.
+      double s = 0.0;
+#pragma unroll
+      for (int j = 0; j < J; j++) {
+        if (!FULL && kWave * j >= G) break;
+        const float4 q = e[j];  // +0 past G
+        const double seg = row16_sum(((double)q.x + (double)q.y) + ((double)q.z + (double)q.w));
+        const double sega = row16_sum(((double)__builtin_fabsf(q.x) + (double)__builtin_fabsf(q.y)) +
+                                      ((double)__builtin_fabsf(q.z) + (double)__builtin_fabsf(q.w)));
+        const int sege = row16_min(min(min(part_ulp_exp(q.x), part_ulp_exp(q.y)),
+                                       min(part_ulp_exp(q.z), part_ulp_exp(q.w))));
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+          if (!FULL && kWave * j + 16 * r >= G) break;
+          const int e_min = min(__builtin_amdgcn_readlane(sege, 16 * r), low_bit_exp(s));
+          if (__builtin_fabs(s) + lane_d(sega, 16 * r) <= exact_limit(e_min)) {
+            s = s + lane_d(seg, 16 * r);
+          } else {
+            for (int i = 16 * r; i < 16 * r + 16; i++) {
+              s = s + (double)lane_f(q.x, i);
+              s = s + (double)lane_f(q.y, i);
+              s = s + (double)lane_f(q.z, i);
+              s = s + (double)lane_f(q.w, i);
+            }
+          }
+        }
+      }
+      for (int l = 0; l < T; l++) s = s + (double)lane_f(et, l);
+      mean = (float)s / fc;
+    }
+  }
+  float part[J];
+#pragma unroll
+  for (int j = 0; j < J; j++) {
+    const int g = lane + kWave * j;
+    e[j] = make_float4(e[j].x - mean, e[j].y - mean, e[j].z - mean, e[j].w - mean);
+    const float q0 = e[j].x * e[j].x, q1 = e[j].y * e[j].y, q2 = e[j].z * e[j].z, q3 = e[j].w * e[j].w;
+    part[j] = (FULL || g < G) ? (q0 + q1) + (q2 + q3) : 0.0f;
+  }
+  const float dt = et - mean, qt = dt * dt;
+  const double dc = (double)cols;
+  const float var = ordered_sum_apply<J, FULL>(part, G, qt, T, [dc](double v) { return (float)(v / dc); });
+  const float scl = 1.0f / sqrtf(var + eps);
+  float v[4 * J];
+#pragma unroll
+  for (int j = 0; j < J; j++) {
+    v[4 * j] = e[j].x * scl;
+    v[4 * j + 1] = e[j].y * scl;
+    v[4 * j + 2] = e[j].z * scl;
+    v[4 * j + 3] = e[j].w * scl;
+  }
+  float tv[1] = {dt * scl};
+  if (EPI) {
+    epi_ops_n(ep, v, w);
+    if (T > 0) epi_ops_n(ep, tv, wt);
+  }
+  float *y = Y + row * cols;
+#pragma unroll
+  for (int j = 0; j < J; j++) {
+    const int g = lane + kWave * j;
+    if (!(FULL || g < G)) continue;
+    float *p = y + 4 * g;
+    if (T == 0) {
+      st4(p, make_float4(v[4 * j], v[4 * j + 1], v[4 * j + 2], v[4 * j + 3]));
+    } else {
+      p[0] = v[4 * j];
+      p[1] = v[4 * j + 1];
+      p[2] = v[4 * j + 2];
+      p[3] = v[4 * j + 3];
+    }
+  }
+  if (lane < T) y[4 * G + lane] = tv[0];
 }
 
 // ---- silu -----------------------------------------------------------------------
@@ -1372,27 +1527,67 @@ ArrayP soft_max(const ArrayP &x0, int64_t rows, int64_t cols, uint32_t scale_bit
   return y;
 }
 
-ArrayP norm(const ArrayP &x0, int64_t rows, int64_t cols, uint32_t eps_bits, bool gpu_ops) {
+ArrayP norm(const ArrayP &x0, int64_t rows, int64_t cols, uint32_t eps_bits, bool gpu_ops,
+            const std::vector<FusedOp> &epi) {
   if (x0->dtype != kF32) fail("ggml.norm: f32 only");
   if (rows * cols != x0->size()) fail("ggml.norm: rows*cols is not the element count");
   if (cols > 4096) fail("ggml.norm: rows above 4096 columns are not carried");
+  if (gpu_ops && !epi.empty()) fail("ggml.norm: no fused ops with the planted binary32 sums");
   ArrayP x = contiguous(x0);
   auto y = new_array(kF32, x->shape);
   if (rows == 0 || cols == 0) return y;
-  // LDS per wave: the row, then its group parts (norm_k's layout); at most
-  // 64 KiB per block.
-  const int per_wave = (int)(cols + 4 + cols / 4 + 4) * (int)sizeof(float);
-  const int waves = std::max(1, std::min(4, 65536 / per_wave));
-  const int lds = waves * per_wave;
-  const unsigned grid = grid_cap(rows, waves, 1 << 20);
   const float *px = (const float *)x->data();
   float *py = (float *)y->data();
   const float eps = bits_f(eps_bits);
-  const int c = (int)cols, go = gpu_ops ? 1 : 0;
+  const int c = (int)cols;
   ArrayP kx = x;
+  if (gpu_ops) {  // planted: binary32 sums and the GPU's own / and sqrt
+    // LDS per wave: the row; at most 64 KiB per block.
+    const int per_wave = (int)(cols + 4) * (int)sizeof(float);
+    const int waves = std::max(1, std::min(4, 65536 / per_wave));
+    const int lds = waves * per_wave;
+    const unsigned grid = grid_cap(rows, waves, 1 << 20);
+    launch([=](hipStream_t s) {
+      (void)kx;
+      norm_planted_k<<<grid, kWave * waves, lds, s>>>(rows, c, eps, px, py);
+    });
+    return y;
+  }
+  std::vector<ArrayP> ek;
+  const Epilogue ep = make_epilogue(epi, &ek);
+  const int J = std::max<int>(1, (int)((cols / 4 + kWave - 1) / kWave));
+  if (ep.n > 0 && J > kNormEpiJ) fail("ggml.norm: fused ops need rows of at most 1024 columns");
+  const bool full = cols == 4LL * kWave * J, fused = ep.n > 0;
+  const int64_t nblk = (rows + 3) / 4;
+  if (nblk > 0x7FFFFFFF) fail("ggml.norm: too many rows");
+  const unsigned grid = (unsigned)nblk;
   launch([=](hipStream_t s) {
-    (void)kx;
-    norm_k<<<grid, kWave * waves, lds, s>>>(rows, c, eps, go, px, py);
+    (void)kx, (void)ek;
+#define NORM_CASE(n)                                                                                    \
+  case n:                                                                                               \
+    if (full) norm_rows_k<n, true, false><<<grid, 256, 0, s>>>(rows, c, eps, ep, px, py);               \
+    else norm_rows_k<n, false, false><<<grid, 256, 0, s>>>(rows, c, eps, ep, px, py);                   \
+    break;
+#define NORM_EPI_CASE(n)                                                                                \
+  case n:                                                                                               \
+    if (full) norm_rows_k<n, true, true><<<grid, 256, 0, s>>>(rows, c, eps, ep, px, py);                \
+    else norm_rows_k<n, false, true><<<grid, 256, 0, s>>>(rows, c, eps, ep, px, py);                    \
+    break;
+    if (fused) {
+      switch (J) {
+        NORM_EPI_CASE(1) NORM_EPI_CASE(2) NORM_EPI_CASE(3) NORM_EPI_CASE(4)
+        default: break;
+      }
+      return;
+    }
+    switch (J) {
+      NORM_CASE(1) NORM_CASE(2) NORM_CASE(3) NORM_CASE(4) NORM_CASE(5) NORM_CASE(6) NORM_CASE(7) NORM_CASE(8)
+      NORM_CASE(9) NORM_CASE(10) NORM_CASE(11) NORM_CASE(12) NORM_CASE(13) NORM_CASE(14) NORM_CASE(15)
+      NORM_CASE(16)
+      default: break;
+    }
+#undef NORM_CASE
+#undef NORM_EPI_CASE
   });
   return y;
 }

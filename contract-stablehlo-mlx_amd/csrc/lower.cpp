@@ -544,13 +544,27 @@ struct Lowerer {
     fail("op " + n + " is not in the lowering table");
   }
 
+  // ggml.norm over the rows of the output's last dim, then `chain` (the fused
+  // prefix at index (0, row, column)).
+  ArrayP run_norm(const Op &o, const ArrayP &x, const std::vector<Chained> &chain) {
+    const std::string attrs = attr_or(o, "composite_attributes", attr_or(o, "backend_config", ""));
+    const Ty &out = o.out_tys.at(0);
+    auto rc = rows_cols(out);
+    std::vector<int64_t> g[3];
+    for (size_t d = 0; d < out.dims.size(); d++) g[d + 1 < out.dims.size() ? 1 : 2].push_back((int64_t)d);
+    const bool can = !f.norm_gpu_ops && rc.second <= 4 * 64 * kNormEpiJ;
+    const std::vector<FusedOp> epi = can ? fusable_prefix(chain, out.dims, g) : std::vector<FusedOp>{};
+    ArrayP y = norm(x, rc.first, rc.second, f32_attr(attrs, "eps"), f.norm_gpu_ops, epi);
+    return apply_chain(reshape(y, out.dims), chain, epi.size());
+  }
+
   std::vector<ArrayP> run_composite(const Op &o, const std::vector<ArrayP> &args) {  // Lower.lean:475-498
     const std::string name = replace_all(attr_or(o, "name", attr_or(o, "call_target_name", "")), "\"", "");
     const std::string attrs = attr_or(o, "composite_attributes", attr_or(o, "backend_config", ""));
     const Ty &out = o.out_tys.at(0);
     auto rc = rows_cols(out);
     const int64_t rows = rc.first, cols = rc.second;
-    if (name == "ggml.norm") return {reshape(norm(args.at(0), rows, cols, f32_attr(attrs, "eps"), f.norm_gpu_ops), out.dims)};
+    if (name == "ggml.norm") return {run_norm(o, args.at(0), {})};
     // A row tail (cols % 4) is refused unless the pinned flavour's correctly
     // rounded expf carries it (Lower.lean:485-486 refuses it always).
     if (name == "ggml.soft_max") {
@@ -569,11 +583,11 @@ struct Lowerer {
   }
 
   // ---- fusion of element-wise chains into their producer (the mx::compile
-  // role): a dot_general whose result's one use is an f32 add / subtract /
-  // multiply / divide / maximum / minimum of the same shape, whose result's
-  // one use is the next such op, and so on, runs as one kernel that applies
-  // the chain to each output before storing it.  Each op is one IEEE rounding
-  // of the same operands, so the bits are those of the separate ops.
+  // role): a dot_general or ggml.norm whose result's one use is an f32 add /
+  // subtract / multiply / divide / maximum / minimum of the same shape, whose
+  // result's one use is the next such op, and so on, runs as one kernel that
+  // applies the chain to each output before storing it.  Each op is one IEEE
+  // rounding of the same operands, so the bits are those of the separate ops.
 
   struct Fusion {
     std::vector<char> skip;               // the producer and the chain's inner ops
@@ -608,10 +622,23 @@ struct Lowerer {
     return true;
   }
 
+  static std::string composite_name(const Op &o) {
+    return replace_all(attr_or(o, "name", attr_or(o, "call_target_name", "")), "\"", "");
+  }
+
+  // A dot_general the lowering accepts, or a ggml.norm (not planted), with one f32 result.
+  bool fusable_producer(const Op &o) const {
+    if (o.results.size() != 1 || o.out_tys.size() != 1 || o.out_tys[0].el != "f32" || o.operands.empty()) return false;
+    std::vector<int64_t> lb, rb, lc, rc;
+    if (o.name == "stablehlo.dot_general") return o.operands.size() == 2 && dot_dims(o, &lb, &rb, &lc, &rc);
+    if (o.name == "stablehlo.composite" || o.name == "stablehlo.custom_call")
+      return composite_name(o) == "ggml.norm" && !f.norm_gpu_ops && o.operands.size() == 1;
+    return false;
+  }
+
   Fusion plan_fusion(const Block &b) const {
     const size_t n = b.ops.size();
     Fusion fu{std::vector<char>(n, 0), std::vector<int>(n, -1), std::vector<std::vector<int>>(n)};
-    if (f.dot_builtin) return fu;
     std::unordered_map<std::string, int> uses, user;
     count_uses(b, &uses);
     for (size_t k = 0; k < n; k++)
@@ -619,10 +646,7 @@ struct Lowerer {
     std::vector<char> claimed(n, 0);
     for (size_t i = 0; i < n; i++) {
       const Op &o = b.ops[i];
-      std::vector<int64_t> lb, rb, lc, rc;
-      if (o.name != "stablehlo.dot_general" || o.results.size() != 1 || !dot_dims(o, &lb, &rb, &lc, &rc) ||
-          o.out_tys[0].el != "f32")
-        continue;
+      if (!fusable_producer(o)) continue;
       const Ty &vt = o.out_tys[0];
       std::string cur = o.results[0];
       std::vector<int> ch;
@@ -657,7 +681,9 @@ struct Lowerer {
       chain.push_back(Chained{c, rev, get(env, e.operands[rev ? 0 : 1])});
       cur = e.results[0];
     }
-    return {dot_general(f, d, get(env, d.operands.at(0)), get(env, d.operands.at(1)), chain)};
+    if (d.name == "stablehlo.dot_general")
+      return {dot_general(f, d, get(env, d.operands.at(0)), get(env, d.operands.at(1)), chain)};
+    return {run_norm(d, get(env, d.operands.at(0)), chain)};
   }
 
   // Run a block whose arguments are `args`, seeing the enclosing env (Lower.lean:503-519).

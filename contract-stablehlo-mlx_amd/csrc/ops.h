@@ -99,8 +99,12 @@ ArrayP mul_mat(const ArrayP &w, const ArrayP &x, int64_t K, int64_t M, int64_t R
 // tail (cols % 4 elements) is carried in the pinned flavour only, through the
 // correctly rounded expf.
 ArrayP soft_max(const ArrayP &x, int64_t rows, int64_t cols, uint32_t scale_bits, bool float_sum);
-// ggml norm (Shaders.lean:130-166).
-ArrayP norm(const ArrayP &x, int64_t rows, int64_t cols, uint32_t eps_bits, bool gpu_ops);
+// ggml norm (Shaders.lean:130-166), then the fused ops `epi` at index
+// (0, row, column) (none with the planted gpu_ops; rows of at most
+// 4 * 64 * kNormEpiJ columns).
+constexpr int kNormEpiJ = 4;
+ArrayP norm(const ArrayP &x, int64_t rows, int64_t cols, uint32_t eps_bits, bool gpu_ops,
+            const std::vector<FusedOp> &epi = {});
 // ggml silu on rows of `cols` (Shaders.lean:172-179); row tails as soft_max.
 ArrayP silu(const ArrayP &x, int64_t rows, int64_t cols, bool gpu_ops);
 // ggml gelu_erf (Shaders.lean:186-199) with a correctly rounded erff.
