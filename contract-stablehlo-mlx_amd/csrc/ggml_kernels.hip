@@ -81,18 +81,32 @@ __device__ __forceinline__ float dot_finish(float a[16], const float *w, int64_t
   return s;
 }
 
+// One operand of a dot kernel: element (b, f, k) at p + boff(b) + f*sf + k*sk,
+// where batch b = b1 * nb2 + b2 sits at b1*sb + b2*sb2 (two batch levels, so
+// per-head views of a [tokens, heads*dh] buffer need no copy; nb2 = 1 for one).
+struct MfmaOperand {
+  const float *p;
+  int64_t sb, sf, sk;
+  int64_t rows;  // N or M
+  int64_t sb2, nb2;
+};
+
+__host__ __device__ __forceinline__ int64_t boff(const MfmaOperand &o, int64_t b) {
+  return o.nb2 == 1 ? b * o.sb : (b / o.nb2) * o.sb + (b % o.nb2) * o.sb2;
+}
+
 // One thread per output; any strides.  The reference kernel's mapping
 // (one thread per output, Shaders.lean:60-64), used for small and irregular
 // shapes and as the parity baseline.
 template <int TAIL>
 __global__ void __launch_bounds__(256) dot_ggml_simple(int64_t n_out, int64_t N, int64_t M, int64_t K,
-                                                       const float *__restrict__ L, int64_t lb, int64_t ln, int64_t lk,
-                                                       const float *__restrict__ R, int64_t rb, int64_t rm, int64_t rk,
-                                                       Epilogue ep, float *__restrict__ y) {
+                                                       MfmaOperand X, MfmaOperand W, Epilogue ep,
+                                                       float *__restrict__ y) {
+  const int64_t lk = X.sk, rk = W.sk;
   for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n_out; i += (int64_t)gridDim.x * blockDim.x) {
     const int64_t m = i % M, t = i / M, n = t % N, b = t / N;
-    const float *x = L + b * lb + n * ln;
-    const float *w = R + b * rb + m * rm;
+    const float *x = X.p + boff(X, b) + n * X.sf;
+    const float *w = W.p + boff(W, b) + m * W.sf;
     if (TAIL == kTailPlain) {  // planted: sequential binary32 sum, no FMA (Shaders.lean:65-68)
       float s = 0.0f;
       for (int64_t k = 0; k < K; k++) {
@@ -167,24 +181,20 @@ constexpr int stash_kind(int load) {
   return load == kLoadRowVecB ? kLoadRowVec : load == kLoadColQuadB ? kLoadColQuad : load;
 }
 
-struct MfmaOperand {
-  const float *p;
-  int64_t sb, sf, sk;
-  int64_t rows;  // N or M
-};
-
 // A buffer loader's per-workgroup state: the batch's buffer resource and the
 // lane's byte offset within it.
 struct BufOp {
   __amdgpu_buffer_rsrc_t r;
   int voff;
+  const float *base;  // the batch's first element (every loader)
 };
 
 template <int LOAD>
 __device__ __forceinline__ BufOp buf_op(const MfmaOperand &o, int64_t b, int64_t r0) {  // any TH <= 512
   BufOp bo;
   const int t = threadIdx.x;
-  bo.r = __builtin_amdgcn_make_buffer_rsrc((void *)(o.p + b * o.sb), (short)0, 0x7FFFFFFF, 0x00020000);
+  bo.base = o.p + boff(o, b);
+  bo.r = __builtin_amdgcn_make_buffer_rsrc((void *)bo.base, (short)0, 0x7FFFFFFF, 0x00020000);
   if (LOAD == kLoadRowVecB) {  // row t / 32, k quad t % 32 (as kLoadRowVec's load 0)
     bo.voff = (int)(((r0 + t / 32) * o.sf + (t % 32) * 4) * 4);
   } else if (LOAD == kLoadColQuadB) {  // row quad (t % 64) / 4, k 4 (t % 4) + 16 (t / 64) (as kLoadColQuad's group 0)
@@ -216,7 +226,7 @@ __device__ __forceinline__ void colquad_coords(int u, int &rq, int &kq) {
 // Registers [I0, I1) of stage s for a workgroup of TH threads (all of it by
 // default; the 4x4 loaders in whole groups of 4).
 template <int LOAD, int TH, int I0 = 0, int I1 = regs_of<TH>()>
-__device__ __forceinline__ void mfma_fetch(const MfmaOperand &o, const BufOp &bo, int64_t b, int64_t r0, int s, int nb,
+__device__ __forceinline__ void mfma_fetch(const MfmaOperand &o, const BufOp &bo, int64_t r0, int s, int nb,
                                            float4 (&reg)[regs_of<TH>()]) {
   static_assert((LOAD != kLoadColQuad && LOAD != kLoadColQuadB) || (I0 % 4 == 0 && I1 % 4 == 0), "whole groups");
   const int t = threadIdx.x;
@@ -247,7 +257,7 @@ __device__ __forceinline__ void mfma_fetch(const MfmaOperand &o, const BufOp &bo
       int64_t row = r0 + 4 * rq;
       if (row > o.rows - 4) row = o.rows - 4;  // stays in bounds (rows % 4 == 0); discarded outputs
       if (k / 16 < nb) {
-        const float *q = o.p + b * o.sb + row + (int64_t)k * o.sk;
+        const float *q = bo.base + row + (int64_t)k * o.sk;
         const float4 v0 = ld4(q), v1 = ld4(q + o.sk), v2 = ld4(q + 2 * o.sk), v3 = ld4(q + 3 * o.sk);
         reg[4 * g + 0] = make_float4(v0.x, v1.x, v2.x, v3.x);
         reg[4 * g + 1] = make_float4(v0.y, v1.y, v2.y, v3.y);
@@ -269,7 +279,7 @@ __device__ __forceinline__ void mfma_fetch(const MfmaOperand &o, const BufOp &bo
       int64_t row = r0 + row_l;
       if (row > o.rows - 1) row = o.rows - 1;  // stays in bounds; those outputs are discarded
       if (k / 16 < nb) {
-        const float *q = o.p + b * o.sb + row + (int64_t)k * o.sk;
+        const float *q = bo.base + row + (int64_t)k * o.sk;
         reg[i] = make_float4(q[0], q[o.sk], q[2 * o.sk], q[3 * o.sk]);
       }
     } else {
@@ -278,7 +288,7 @@ __device__ __forceinline__ void mfma_fetch(const MfmaOperand &o, const BufOp &bo
       int64_t row = r0 + row_l;
       if (row > o.rows - 1) row = o.rows - 1;
       if (k / 16 < nb) {
-        const float *q = o.p + b * o.sb + row * o.sf;
+        const float *q = bo.base + row * o.sf;
         if (LOAD == kLoadRowVec) {
           reg[i] = ld4(q + k);
         } else {
@@ -356,8 +366,8 @@ __device__ __forceinline__ void dot_store_rows(const MfmaOperand &X, const MfmaO
     for (int r = 0; r < 8; r++) {
       const int64_t nr = n + 8 * (r / 4) + r % 4;
       if (nr >= N) continue;
-      const float *xr = X.p + b * X.sb + nr * X.sf;
-      const float *wr = W.p + b * W.sb + m * W.sf;
+      const float *xr = X.p + boff(X, b) + nr * X.sf;
+      const float *wr = W.p + boff(W, b) + m * W.sf;
       float sumf = v[r];
       if (tail == kTailPinned) {
         for (int64_t k = np; k < K; k++) {
@@ -419,8 +429,8 @@ __global__ void __launch_bounds__(512) dot_mfma8_k(MfmaOperand X, MfmaOperand W,
   float4 rx[R], rw[R];
   const BufOp bx = buf_op<LX>(X, b, n0), bw = buf_op<LW>(W, b, m0);
   if (nst > 0) {
-    mfma_fetch<LX, TH>(X, bx, b, n0, 0, nb, rx);
-    mfma_fetch<LW, TH>(W, bw, b, m0, 0, nb, rw);
+    mfma_fetch<LX, TH>(X, bx, n0, 0, nb, rx);
+    mfma_fetch<LW, TH>(W, bw, m0, 0, nb, rw);
     mfma_stash<LX, TH>(tile(0, 0), rx);
     mfma_stash<LW, TH>(tile(0, 1), rw);
   }
@@ -449,8 +459,8 @@ __global__ void __launch_bounds__(512) dot_mfma8_k(MfmaOperand X, MfmaOperand W,
     const bool more = s + 1 < nst;
     auto part = [&](int q) {
       if (more) {
-        if (q == 0) mfma_fetch<LX, TH>(X, bx, b, n0, s + 1, nb, rx);
-        if (q == 1) mfma_fetch<LW, TH>(W, bw, b, m0, s + 1, nb, rw);
+        if (q == 0) mfma_fetch<LX, TH>(X, bx, n0, s + 1, nb, rx);
+        if (q == 1) mfma_fetch<LW, TH>(W, bw, m0, s + 1, nb, rw);
         if (q == 4) mfma_stash<LX, TH>(tile(buf ^ 1, 0), rx);
         if (q == 5) mfma_stash<LW, TH>(tile(buf ^ 1, 1), rw);
       }
@@ -551,8 +561,8 @@ __global__ void __launch_bounds__(512) dot_mfma8p_k(MfmaOperand X, MfmaOperand W
 
   float4 rx[R], rw[R];
   if (nst > 0) {
-    mfma_fetch<LX, TH>(X, bx, b, n0, 0, nb, rx);
-    mfma_fetch<LW, TH>(W, bw, b, m0, 0, nb, rw);
+    mfma_fetch<LX, TH>(X, bx, n0, 0, nb, rx);
+    mfma_fetch<LW, TH>(W, bw, m0, 0, nb, rw);
     mfma_stash<LX, TH>(tile(0, 0), rx);
     mfma_stash<LW, TH>(tile(0, 1), rw);
   }
@@ -577,7 +587,7 @@ __global__ void __launch_bounds__(512) dot_mfma8p_k(MfmaOperand X, MfmaOperand W
       const bool here = s + 1 < nst;
       const bool more = here || has_next;
       const int fs = here ? s + 1 : 0;
-      const int64_t fb = here ? b : nb_, fn0 = here ? n0 : nn0, fm0 = here ? m0 : nm0;
+      const int64_t fn0 = here ? n0 : nn0, fm0 = here ? m0 : nm0;
       const BufOp &fbx = here ? bx : nbx;
       const BufOp &fbw = here ? bw : nbw;
       // As in dot_mfma8_k: straight-line blocks, block blk + 1's operands read
@@ -594,8 +604,8 @@ __global__ void __launch_bounds__(512) dot_mfma8p_k(MfmaOperand X, MfmaOperand W
       };
       auto part = [&](int q) {
         if (more) {
-          if (q == 0) mfma_fetch<LX, TH>(X, fbx, fb, fn0, fs, nb, rx);
-          if (q == 1) mfma_fetch<LW, TH>(W, fbw, fb, fm0, fs, nb, rw);
+          if (q == 0) mfma_fetch<LX, TH>(X, fbx, fn0, fs, nb, rx);
+          if (q == 1) mfma_fetch<LW, TH>(W, fbw, fm0, fs, nb, rw);
           if (q == 4) mfma_stash<LX, TH>(tile(buf ^ 1, 0), rx);
           if (q == 5) mfma_stash<LW, TH>(tile(buf ^ 1, 1), rw);
         }
@@ -800,6 +810,7 @@ __device__ __forceinline__ float ordered_sum_apply(const float (&part)[J], int G
       if (t <= lim_p && (s == 0.0 || t <= lim_s)) {
         s = t;
       } else {
+#pragma unroll 1
         for (int i = 0; i < 16; i++) s = s + (double)lane_f(part[j], 16 * r + i);
       }
     }
@@ -1119,6 +1130,7 @@ __global__ void __launch_bounds__(256) norm_rows_k(int64_t rows, int cols, float
           if (__builtin_fabs(s) + lane_d(sega, 16 * r) <= exact_limit(e_min)) {
             s = s + lane_d(seg, 16 * r);
           } else {
+#pragma unroll 1
             for (int i = 16 * r; i < 16 * r + 16; i++) {
               s = s + (double)lane_f(q.x, i);
               s = s + (double)lane_f(q.y, i);
@@ -1350,21 +1362,23 @@ ArrayP dot_ggml(const DotOperand &lhs, const DotOperand &rhs, int64_t B, int64_t
   float *Y = (float *)y->data();
   ArrayP kl = lhs.arr, kr = rhs.arr;
   const int64_t lb = lhs.sb, ln = lhs.sf, lk = lhs.sk, rb = rhs.sb, rm = rhs.sf, rk = rhs.sk;
+  if (lhs.nb2 < 1 || rhs.nb2 < 1 || B % lhs.nb2 || B % rhs.nb2) fail("dot_general: inner batch count does not divide");
+  const MfmaOperand X{L, lb, ln, lk, N, lhs.sb2, lhs.nb2}, W{R, rb, rm, rk, M, rhs.sb2, rhs.nb2};
   if (tail != kTailPlain && B <= 65535) {
-    auto loader = [&](const float *p, int64_t sb, int64_t sf, int64_t sk, int64_t rows) {
-      const bool al = ((uintptr_t)p % 16) == 0 && (sb % 4 == 0 || B == 1);
+    auto loader = [&](const float *p, int64_t sb, int64_t sf, int64_t sk, int64_t rows, const DotOperand &d) {
+      const bool al = ((uintptr_t)p % 16) == 0 && (sb % 4 == 0 || B == 1) && (d.nb2 == 1 || d.sb2 % 4 == 0);
       if (al && sk == 1 && (sf % 4 == 0 || rows == 1)) return (int)kLoadRowVec;
       if (al && sf == 1 && sk % 4 == 0 && rows % 4 == 0) return (int)kLoadColQuad;
       if (sf == 1) return (int)kLoadColVec;
       return (int)kLoadScalar;
     };
-    int lx = loader(L, lb, ln, lk, N), lw = loader(R, rb, rm, rk, M);
+    int lx = loader(L, lb, ln, lk, N, lhs), lw = loader(R, rb, rm, rk, M, rhs);
     // The buffer loaders need every read in range by construction: rows a
     // multiple of the tile, every stage full, non-negative strides, and the
     // largest byte offset within a batch below 2^31.
     const bool full_stages = ((K / 16) % (kKC / 16)) == 0 && K >= kKC;
     auto buf_ok = [&](int64_t sf, int64_t sk, int64_t sb, int64_t rows) {
-      if (rows % kMT || !full_stages || sf < 0 || sk < 0 || sb < 0) return false;
+      if (rows % kMT || !full_stages || sf < 0 || sk < 0 || sb < 0 || lhs.sb2 < 0 || rhs.sb2 < 0) return false;
       const int64_t top = ((rows - 1) * sf + (K - 1) * sk + 4) * 4;
       return top < ((int64_t)1 << 31);
     };
@@ -1391,7 +1405,6 @@ ArrayP dot_ggml(const DotOperand &lhs, const DotOperand &rhs, int64_t B, int64_t
       return true;
     }();
     (void)lds_ok;
-    const MfmaOperand X{L, lb, ln, lk, N}, W{R, rb, rm, rk, M};
     const int tiles_m = (int)((M + kMT - 1) / kMT);
     const int64_t tiles_b = ((N + kMT - 1) / kMT) * tiles_m, tiles = B * tiles_b;
     if (tiles_m > 0x7FFFFFFF || tiles / std::max<int64_t>(B, 1) != tiles_b) fail("dot_general: too many output tiles");
@@ -1431,13 +1444,13 @@ ArrayP dot_ggml(const DotOperand &lhs, const DotOperand &rhs, int64_t B, int64_t
     (void)kl, (void)kr, (void)ek;
     switch (tail) {
       case kTailStock:
-        dot_ggml_simple<kTailStock><<<grid, 256, 0, s>>>(n_out, N, M, K, L, lb, ln, lk, R, rb, rm, rk, ep, Y);
+        dot_ggml_simple<kTailStock><<<grid, 256, 0, s>>>(n_out, N, M, K, X, W, ep, Y);
         break;
       case kTailPinned:
-        dot_ggml_simple<kTailPinned><<<grid, 256, 0, s>>>(n_out, N, M, K, L, lb, ln, lk, R, rb, rm, rk, ep, Y);
+        dot_ggml_simple<kTailPinned><<<grid, 256, 0, s>>>(n_out, N, M, K, X, W, ep, Y);
         break;
       default:
-        dot_ggml_simple<kTailPlain><<<grid, 256, 0, s>>>(n_out, N, M, K, L, lb, ln, lk, R, rb, rm, rk, ep, Y);
+        dot_ggml_simple<kTailPlain><<<grid, 256, 0, s>>>(n_out, N, M, K, X, W, ep, Y);
         break;
     }
   });

@@ -181,12 +181,30 @@ DotOperand dot_operand(const ArrayP &a, const std::vector<int64_t> &batch, const
                        int64_t contract) {
   DotOperand op;
   int64_t sb = 0, sf = 0;
-  if (flat_stride(a, batch, &sb) && flat_stride(a, free, &sf)) {
-    op.arr = a;
-    op.sb = sb;
-    op.sf = sf;
-    op.sk = a->strides[contract];
-    return op;
+  if (flat_stride(a, free, &sf)) {
+    if (flat_stride(a, batch, &sb)) {
+      op.arr = a;
+      op.sb = sb;
+      op.sf = sf;
+      op.sk = a->strides[contract];
+      return op;
+    }
+    // Two batch levels: outer dims [0, k) and inner dims [k, end), each flat
+    // (per-head views such as [B, H, T, dh] over a [B, T, H*dh] buffer).
+    for (size_t k = 1; k < batch.size(); k++) {
+      const std::vector<int64_t> outer(batch.begin(), batch.begin() + k), inner(batch.begin() + k, batch.end());
+      int64_t s1 = 0, s2 = 0, n2 = 1;
+      for (int64_t d : inner) n2 *= a->shape[d];
+      if (n2 > 1 && flat_stride(a, outer, &s1) && flat_stride(a, inner, &s2)) {
+        op.arr = a;
+        op.sb = s1;
+        op.sb2 = s2;
+        op.nb2 = n2;
+        op.sf = sf;
+        op.sk = a->strides[contract];
+        return op;
+      }
+    }
   }
   // Not flattenable: copy to [batch, free, contract] (the reference's layout).
   std::vector<int64_t> perm(batch);

@@ -67,9 +67,12 @@ void set_default_dot_tail(int);  // 0 stock (the reference kernel), 1 pinned
 
 // One operand of a dot product, addressed as (batch, free, k) with element
 // strides: element (b, f, k) is at data + b*sb + f*sf + k*sk.
+// With nb2 > 1 the batch index b = b1 * nb2 + b2 takes two strides:
+// element (b, f, k) is at data + b1*sb + b2*sb2 + f*sf + k*sk.
 struct DotOperand {
   ArrayP arr;       // keeps the buffer alive
   int64_t sb = 0, sf = 0, sk = 0;
+  int64_t sb2 = 0, nb2 = 1;
 };
 
 // One element-wise binary32 op fused into a producer's store: v = op(v, o)

@@ -16,11 +16,55 @@ static std::shared_ptr<Array> view_of(const ArrayP &a) {
 
 ArrayP empty_array() { return new_array(kF32, Shape{0}); }
 
+// Strides for viewing an array of shape `os` / strides `ost` as `ns` without
+// moving data, when they exist: old and new dims are matched in groups of
+// equal element count (outer to inner, size-1 old dims dropped); each group's
+// old dims must nest (stride[i] == stride[i+1] * shape[i+1]), and its new
+// dims then take strides from the group's innermost one (numpy's no-copy
+// reshape rule).  A slice's rows split into heads, for one, stay a view.
+static bool reshape_strides(const Shape &os, const Shape &ost, const Shape &ns, Shape *nst) {
+  Shape od, ostr;
+  for (size_t i = 0; i < os.size(); i++)
+    if (os[i] != 1) od.push_back(os[i]), ostr.push_back(ost[i]);
+  nst->assign(ns.size(), 0);
+  size_t oi = 0, ni = 0;
+  while (oi < od.size() && ni < ns.size()) {
+    int64_t np = ns[ni], op = od[oi];
+    size_t nj = ni + 1, oj = oi + 1;
+    while (np != op) {
+      if (np < op) {
+        if (nj == ns.size()) return false;
+        np *= ns[nj++];
+      } else {
+        if (oj == od.size()) return false;
+        op *= od[oj++];
+      }
+    }
+    for (size_t k = oi; k + 1 < oj; k++)
+      if (ostr[k] != ostr[k + 1] * od[k + 1]) return false;
+    (*nst)[nj - 1] = ostr[oj - 1];
+    for (size_t k = nj - 1; k > ni; k--) (*nst)[k - 1] = (*nst)[k] * ns[k];
+    oi = oj;
+    ni = nj;
+  }
+  if (oi != od.size()) return false;
+  for (; ni < ns.size(); ni++)
+    if (ns[ni] != 1) return false;
+  return true;
+}
+
 ArrayP reshape(const ArrayP &a, const Shape &shape) {
   if ((int)shape.size() > kMaxRank) fail("reshape: rank above 16");
   if (shape_count(shape) != a->size())
     fail(strf("reshape: %s has %lld elements, %s asks for %lld", shape_str(a->shape).c_str(),
               (long long)a->size(), shape_str(shape).c_str(), (long long)shape_count(shape)));
+  Shape st;
+  if (!a->contiguous() && a->size() > 0 && reshape_strides(a->shape, a->strides, shape, &st)) {
+    auto v = view_of(a);
+    v->shape = shape;
+    v->strides = st;
+    return v;
+  }
   ArrayP src = a->contiguous() ? a : contiguous(a);
   auto v = view_of(src);
   v->shape = shape;

@@ -153,3 +153,72 @@ def test_views_and_data_movement():
     i32 = shlo_hip.astype(A, shlo_hip.I32).numpy()
     assert np.array_equal(i32, a.astype(np.int32))
     assert np.array_equal(shlo_hip.view(A, shlo_hip.U32).numpy(), a.view(np.uint32))
+
+
+def test_reshape_keeps_views_where_strides_nest():
+    """A reshape of a strided view shares its buffer when every group of
+    merged or split dims nests (a slice's rows split into heads, a
+    transpose's last dim split), and copies when it does not; the values are
+    numpy's either way, and element-wise kernels read the strided result."""
+    import shlo_hip
+    a = np.arange(4 * 6 * 8, dtype=np.float32).reshape(4, 6, 8)
+    A = shlo_hip.from_numpy(a)
+    S = shlo_hip.slice_(A, (0, 0, 2), (4, 6, 6), (1, 1, 1))
+    s = a[:, :, 2:6]
+    T = shlo_hip.transpose(A, (1, 0, 2))
+    t = a.transpose(1, 0, 2)
+    cases = [(S, s, (24, 4), True), (S, s, (4, 6, 2, 2), True), (S, s, (1, 4, 1, 6, 4, 1), True),
+             (S, s, (4, 24), False), (S, s, (96,), False), (T, t, (6, 4, 2, 4), True), (T, t, (24, 8), False),
+             (T, t, (6, 32), False)]
+    for X, x, shape, view in cases:
+        R = shlo_hip.reshape(X, shape)
+        assert same_bits(R.numpy(), x.reshape(shape)), shape
+        assert (R.data_ptr() == X.data_ptr()) == view, (shape, view)
+        assert same_bits(shlo_hip.binary("add", R, R).numpy(), (x + x).reshape(shape)), shape
+
+
+def test_attention_heads_from_one_projection(oracle):
+    """q, k, v as per-head views of one [tokens, 3d] projection (slice,
+    reshape, transpose, as the denoiser builds them): the products read them
+    in place through two batch strides; both flavours, eager and compiled,
+    against the oracle on copied operands."""
+    import shlo_hip
+    B, T, H, dh = 2, 96, 3, 64
+    d, tok = H * dh, B * T
+    qkv, _ = oracle.fill_normal(61, 1.0, tok * 3 * d)
+    qkv = qkv.reshape(tok, 3 * d)
+
+    def ty(*s):
+        return "tensor<" + "".join(f"{x}x" for x in s) + "f32>"
+
+    lines = []
+    for i, nm in enumerate("qkv"):
+        lines.append(f'    %{nm}s = "stablehlo.slice"(%x) {{start_indices = array<i64: 0, {i * d}>, limit_indices = '
+                     f'array<i64: {tok}, {(i + 1) * d}>, strides = array<i64: 1, 1>}} : ({ty(tok, 3 * d)}) -> {ty(tok, d)}\n'
+                     f'    %{nm}r = "stablehlo.reshape"(%{nm}s) : ({ty(tok, d)}) -> {ty(B, T, H, dh)}\n'
+                     f'    %{nm} = "stablehlo.transpose"(%{nm}r) {{permutation = array<i64: 0, 2, 1, 3>}} : '
+                     f"({ty(B, T, H, dh)}) -> {ty(B, H, T, dh)}\n")
+    dn_qk = ("#stablehlo.dot<lhs_batching_dimensions = [0, 1], rhs_batching_dimensions = [0, 1], "
+             "lhs_contracting_dimensions = [3], rhs_contracting_dimensions = [3]>")
+    dn_pv = ("#stablehlo.dot<lhs_batching_dimensions = [0, 1], rhs_batching_dimensions = [0, 1], "
+             "lhs_contracting_dimensions = [3], rhs_contracting_dimensions = [2]>")
+    text = (f"module {{\n  func.func public @main(%x: {ty(tok, 3 * d)}) -> ({ty(B, H, T, T)}, {ty(B, H, T, dh)}) {{\n" +
+            "".join(lines) +
+            f'    %s = "stablehlo.dot_general"(%q, %k) {{dot_dimension_numbers = {dn_qk}}} : '
+            f"({ty(B, H, T, dh)}, {ty(B, H, T, dh)}) -> {ty(B, H, T, T)}\n"
+            f'    %o = "stablehlo.dot_general"(%s, %v) {{dot_dimension_numbers = {dn_pv}}} : '
+            f"({ty(B, H, T, T)}, {ty(B, H, T, dh)}) -> {ty(B, H, T, dh)}\n"
+            f"    func.return %s, %o : {ty(B, H, T, T)}, {ty(B, H, T, dh)}\n  }}\n}}\n")
+    heads = qkv.reshape(B, T, 3, H, dh).transpose(2, 0, 3, 1, 4)  # [3, B, H, T, dh]
+    q, k, v = (np.ascontiguousarray(heads[i]).reshape(B * H, T, dh) for i in range(3))
+    for flavor in (0, 1):
+        s_want = oracle.dot_general_bnk(q, k, flavor)
+        o_want = oracle.dot_general_bnk(s_want, np.ascontiguousarray(v.transpose(0, 2, 1)), flavor)
+        shlo_hip.set_flavor(flavor)
+        try:
+            for compile in (True, False):
+                got = shlo_hip.Module(text).prepare(0, compile).call([shlo_hip.from_numpy(qkv)])
+                assert same_bits(got[0].numpy(), s_want.reshape(B, H, T, T)), (flavor, compile)
+                assert same_bits(got[1].numpy(), o_want.reshape(B, H, T, dh)), (flavor, compile)
+        finally:
+            shlo_hip.set_flavor(0)
