@@ -91,8 +91,10 @@ struct MfmaOperand {
   int64_t sb2, nb2;
 };
 
-__host__ __device__ __forceinline__ int64_t boff(const MfmaOperand &o, int64_t b) {
-  return o.nb2 == 1 ? b * o.sb : (b / o.nb2) * o.sb + (b % o.nb2) * o.sb2;
+__host__ __device__ __forceinline__ int64_t boff(const MfmaOperand &o, int64_t b) {  // b < 2^31 (the host checks)
+  if (o.nb2 == 1) return b * o.sb;
+  const uint32_t q = (uint32_t)b / (uint32_t)o.nb2, r = (uint32_t)b - q * (uint32_t)o.nb2;
+  return (int64_t)q * o.sb + (int64_t)r * o.sb2;
 }
 
 // One thread per output; any strides.  The reference kernel's mapping
@@ -350,6 +352,16 @@ __device__ __forceinline__ void mfma_block4(v32f (&acc)[4], const float4 &a, con
   acc[3] = __builtin_amdgcn_mfma_f32_32x32x1f32(a.w, b.w, acc[3], 0, 0, 0);
 }
 
+// A tile's first block: the accumulators start from +0 as ggml's do, given
+// as the instruction's inline zero operand instead of 128 register moves.
+__device__ __forceinline__ void mfma_block4_first(v32f (&acc)[4], const float4 &a, const float4 &b) {
+  const v32f z = {};
+  acc[0] = __builtin_amdgcn_mfma_f32_32x32x1f32(a.x, b.x, z, 0, 0, 0);
+  acc[1] = __builtin_amdgcn_mfma_f32_32x32x1f32(a.y, b.y, z, 0, 0, 0);
+  acc[2] = __builtin_amdgcn_mfma_f32_32x32x1f32(a.z, b.z, z, 0, 0, 0);
+  acc[3] = __builtin_amdgcn_mfma_f32_32x32x1f32(a.w, b.w, z, 0, 0, 0);
+}
+
 // Stores the 8 outputs a lane finishes: rows n + 8 (r / 4) + r % 4 of column m
 // (r = 0..7), after the serial tail of dot_finish when K % 16 != 0 and the
 // fused element-wise ops.  `whole` (wave-uniform) says every output is in
@@ -421,10 +433,12 @@ __global__ void __launch_bounds__(512) dot_mfma8_k(MfmaOperand X, MfmaOperand W,
   const int nst = (nb + kKC / 16 - 1) / (kKC / 16);
 
   v32f acc[4];
+  if (nst == 0) {  // K < 16: no block; the tail starts from the +0 tree
 #pragma unroll
-  for (int q = 0; q < 4; q++)
+    for (int q = 0; q < 4; q++)
 #pragma unroll
-    for (int r = 0; r < 32; r++) acc[q][r] = 0.0f;
+      for (int r = 0; r < 32; r++) acc[q][r] = 0.0f;
+  }
 
   float4 rx[R], rw[R];
   const BufOp bx = buf_op<LX>(X, b, n0), bw = buf_op<LW>(W, b, m0);
@@ -472,7 +486,8 @@ __global__ void __launch_bounds__(512) dot_mfma8_k(MfmaOperand X, MfmaOperand W,
     for (int blk = 0; blk < kKC / 16; blk += 2) {
       rd(blk + 1, pb, qb);
       __builtin_amdgcn_sched_barrier(0);
-      if (blk < blocks) mfma_block4(acc, pa, qa);
+      if (blk == 0 && s == 0) mfma_block4_first(acc, pa, qa);
+      else if (blk < blocks) mfma_block4(acc, pa, qa);
       if (blk == 0 || blk == 4) part(blk);
       if (blk + 2 < kKC / 16) rd(blk + 2, pa, qa);
       __builtin_amdgcn_sched_barrier(0);
@@ -520,6 +535,14 @@ __device__ __forceinline__ float2 ld2_lds_v(const float *p) {
   return make_float2(v.x, v.y);
 }
 
+// The persistent kernel's tile walk: tiles (b, nt, mt) in row-major order over
+// (B, tiles_n, tiles_m), and gridDim.x = (db * tiles_n + dnt) * tiles_m + dmt
+// with dnt < tiles_n, dmt < tiles_m.
+struct TileWalk {
+  int64_t tiles;
+  int tiles_n, tiles_m, db, dnt, dmt;
+};
+
 // Persistent form: one workgroup per CU walks output tiles t = blockIdx.x,
 // blockIdx.x + gridDim.x, ..., and its stage pipeline runs straight across
 // tile boundaries, so the next tile's loads and LDS writes overlap this
@@ -540,8 +563,7 @@ __device__ __forceinline__ float2 ld2_lds_v(const float *p) {
 // share of a tile (short K); dot_mfma8_k's float4 reads where it is not.
 template <int LX, int LW>
 __global__ void __launch_bounds__(512) dot_mfma8p_k(MfmaOperand X, MfmaOperand W, int64_t N, int64_t M, int64_t K,
-                                                    int tail, int tiles_m, int64_t tiles_b, int64_t tiles,
-                                                    Epilogue ep, float *__restrict__ Y) {
+                                                    int tail, TileWalk tw, Epilogue ep, float *__restrict__ Y) {
   constexpr int TH = 512, R = regs_of<TH>();
   extern __shared__ float lds_m[];  // [buffer][operand][kMT * kLS]
   auto tile = [&](int buf, int op) { return lds_m + (buf * 2 + op) * (kMT * kLS); };
@@ -552,11 +574,12 @@ __global__ void __launch_bounds__(512) dot_mfma8p_k(MfmaOperand X, MfmaOperand W
   const int64_t np = K & ~(int64_t)15;
   const int nb = (int)(np / 16);
   const int nst = (nb + kKC / 16 - 1) / (kKC / 16);
+  // Tile t = (b * tiles_n + nt) * tiles_m + mt; t advances by gridDim.x, whose
+  // digits in that mixed radix the host passes (no division per tile).
   int64_t t = blockIdx.x;  // the host launches at most `tiles` workgroups
-  auto tile_b = [&](int64_t tt) { return tt / tiles_b; };
-  auto tile_n0 = [&](int64_t tt) { return ((tt % tiles_b) / tiles_m) * kMT; };
-  auto tile_m0 = [&](int64_t tt) { return ((tt % tiles_b) % tiles_m) * kMT; };
-  int64_t b = tile_b(t), n0 = tile_n0(t), m0 = tile_m0(t);
+  const int tiles_b = tw.tiles_n * tw.tiles_m;
+  int b = (int)blockIdx.x / tiles_b, nt = ((int)blockIdx.x % tiles_b) / tw.tiles_m, mt = (int)blockIdx.x % tw.tiles_m;
+  int64_t n0 = (int64_t)nt * kMT, m0 = (int64_t)mt * kMT;
   BufOp bx = buf_op<LX>(X, b, n0), bw = buf_op<LW>(W, b, m0);
 
   float4 rx[R], rw[R];
@@ -570,14 +593,19 @@ __global__ void __launch_bounds__(512) dot_mfma8p_k(MfmaOperand X, MfmaOperand W
   int buf = 0;
   v32f acc[4];
   for (;;) {
+    if (nst == 0) {  // K < 16: no block; the tail starts from the +0 tree
 #pragma unroll
-    for (int q = 0; q < 4; q++)
+      for (int q = 0; q < 4; q++)
 #pragma unroll
-      for (int r = 0; r < 32; r++) acc[q][r] = 0.0f;
+        for (int r = 0; r < 32; r++) acc[q][r] = 0.0f;
+    }
     const int64_t tn = t + gridDim.x;
-    const bool has_next = tn < tiles;
-    const int64_t nb_ = has_next ? tile_b(tn) : b, nn0 = has_next ? tile_n0(tn) : n0,
-                  nm0 = has_next ? tile_m0(tn) : m0;
+    const bool has_next = tn < tw.tiles;
+    int mt_ = mt + tw.dmt, nt_ = nt + tw.dnt, b_ = b + tw.db;
+    if (mt_ >= tw.tiles_m) mt_ -= tw.tiles_m, nt_++;
+    if (nt_ >= tw.tiles_n) nt_ -= tw.tiles_n, b_++;
+    const int nb_ = has_next ? b_ : b;
+    const int64_t nn0 = has_next ? (int64_t)nt_ * kMT : n0, nm0 = has_next ? (int64_t)mt_ * kMT : m0;
     const BufOp nbx = buf_op<LX>(X, nb_, nn0), nbw = buf_op<LW>(W, nb_, nm0);
     for (int s = 0; s < nst; s++) {
       const float *xs = tile(buf, 0) + (wn * 32 + li) * kLS + 8 * h + 2 * rh;
@@ -617,7 +645,8 @@ __global__ void __launch_bounds__(512) dot_mfma8p_k(MfmaOperand X, MfmaOperand W
       for (int blk = 0; blk < kKC / 16; blk += 2) {
         rd(blk + 1, pb, qb);
         __builtin_amdgcn_sched_barrier(0);
-        if (blk < blocks) mfma_block4(acc, pa, qa);
+        if (blk == 0 && s == 0) mfma_block4_first(acc, pa, qa);
+        else if (blk < blocks) mfma_block4(acc, pa, qa);
         if (blk == 0 || blk == 4) part(blk);
         if (blk + 2 < kKC / 16) rd(blk + 2, pa, qa);
         __builtin_amdgcn_sched_barrier(0);
@@ -656,7 +685,9 @@ __global__ void __launch_bounds__(512) dot_mfma8p_k(MfmaOperand X, MfmaOperand W
     __syncthreads();  // the exchange's buffer takes the stage after next's LDS writes
     if (!has_next) break;
     t = tn;
-    b = nb_;
+    b = b_;
+    nt = nt_;
+    mt = mt_;
     n0 = nn0;
     m0 = nm0;
     bx = nbx;
@@ -1363,6 +1394,7 @@ ArrayP dot_ggml(const DotOperand &lhs, const DotOperand &rhs, int64_t B, int64_t
   ArrayP kl = lhs.arr, kr = rhs.arr;
   const int64_t lb = lhs.sb, ln = lhs.sf, lk = lhs.sk, rb = rhs.sb, rm = rhs.sf, rk = rhs.sk;
   if (lhs.nb2 < 1 || rhs.nb2 < 1 || B % lhs.nb2 || B % rhs.nb2) fail("dot_general: inner batch count does not divide");
+  if (B > 0x7FFFFFFF) fail("dot_general: more than 2^31 - 1 batches");
   const MfmaOperand X{L, lb, ln, lk, N, lhs.sb2, lhs.nb2}, W{R, rb, rm, rk, M, rhs.sb2, rhs.nb2};
   if (tail != kTailPlain && B <= 65535) {
     auto loader = [&](const float *p, int64_t sb, int64_t sf, int64_t sk, int64_t rows, const DotOperand &d) {
@@ -1405,9 +1437,11 @@ ArrayP dot_ggml(const DotOperand &lhs, const DotOperand &rhs, int64_t B, int64_t
       return true;
     }();
     (void)lds_ok;
-    const int tiles_m = (int)((M + kMT - 1) / kMT);
-    const int64_t tiles_b = ((N + kMT - 1) / kMT) * tiles_m, tiles = B * tiles_b;
-    if (tiles_m > 0x7FFFFFFF || tiles / std::max<int64_t>(B, 1) != tiles_b) fail("dot_general: too many output tiles");
+    const int64_t tiles_m64 = (M + kMT - 1) / kMT, tiles_n64 = (N + kMT - 1) / kMT;
+    if (tiles_m64 > 0x7FFFFFFF || tiles_n64 > 0x7FFFFFFF || tiles_m64 * tiles_n64 > 0x7FFFFFFF)
+      fail("dot_general: too many output tiles");
+    const int tiles_m = (int)tiles_m64;
+    const int64_t tiles_b = tiles_n64 * tiles_m64, tiles = B * tiles_b;
     // Short contractions (up to kPersistStages stages of 128) run the
     // persistent kernel with the one-value exchange, whose next tile's loads
     // hide under this tile's epilogue (attention 0.173 ms against 0.189 one
@@ -1416,6 +1450,8 @@ ArrayP dot_ggml(const DotOperand &lhs, const DotOperand &rhs, int64_t B, int64_t
     const int64_t stages = (K / 16 + kKC / 16 - 1) / (kKC / 16);
     const bool persist = stages <= kPersistStages;
     const unsigned grid = (unsigned)std::min<int64_t>(tiles, device_props().multiProcessorCount);  // one per CU
+    TileWalk tw{tiles, (int)tiles_n64, tiles_m, (int)(grid / tiles_b), (int)((grid % tiles_b) / tiles_m64),
+                (int)(grid % tiles_m64)};
     const dim3 grid1((unsigned)tiles_b, (unsigned)B);
     if (!persist && tiles_b > 0x7FFFFFFF) fail("dot_general: too many output tiles");
     const int tl = tail;
@@ -1423,7 +1459,7 @@ ArrayP dot_ggml(const DotOperand &lhs, const DotOperand &rhs, int64_t B, int64_t
       (void)kl, (void)kr, (void)ek;
 #define DOT_CASE(a, c)                                                                    \
   if (lx == a && lw == c) {                                                               \
-    if (persist) dot_mfma8p_k<a, c><<<grid, 512, kDotLds, s>>>(X, W, N, M, K, tl, tiles_m, tiles_b, tiles, ep, Y); \
+    if (persist) dot_mfma8p_k<a, c><<<grid, 512, kDotLds, s>>>(X, W, N, M, K, tl, tw, ep, Y);           \
     else dot_mfma8_k<a, c><<<grid1, 512, kDotLds, s>>>(X, W, N, M, K, tl, tiles_m, ep, Y);                  \
     return;                                                                               \
   }
