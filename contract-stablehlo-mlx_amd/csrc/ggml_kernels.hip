@@ -362,24 +362,25 @@ __device__ __forceinline__ void mfma_block4_first(v32f (&acc)[4], const float4 &
   acc[3] = __builtin_amdgcn_mfma_f32_32x32x1f32(a.w, b.w, z, 0, 0, 0);
 }
 
-// Stores the 8 outputs a lane finishes: rows n + 8 (r / 4) + r % 4 of column m
-// (r = 0..7), after the serial tail of dot_finish when K % 16 != 0 and the
-// fused element-wise ops.  `whole` (wave-uniform) says every output is in
-// range and there is no tail.
-__device__ __forceinline__ void dot_store_rows(const MfmaOperand &X, const MfmaOperand &W, int64_t b, int64_t n,
-                                               int64_t m, int64_t N, int64_t M, int64_t K, int64_t np, int tail,
-                                               bool whole, const float (&out)[8], const Epilogue &ep,
-                                               float *__restrict__ Y) {
+// Stores the 8 outputs a lane finishes, output r at row row(r) and column
+// col(r), after the serial tail of dot_finish when K % 16 != 0 and the fused
+// element-wise ops.  `whole` (wave-uniform) says every output is in range and
+// there is no tail.
+template <class RowF, class ColF>
+__device__ __forceinline__ void dot_store8(const MfmaOperand &X, const MfmaOperand &W, int64_t b, int64_t N,
+                                           int64_t M, int64_t K, int64_t np, int tail, bool whole,
+                                           const float (&out)[8], const Epilogue &ep, float *__restrict__ Y, RowF row,
+                                           ColF col) {
   float v[8];
 #pragma unroll
   for (int r = 0; r < 8; r++) v[r] = out[r];
-  if (!whole && np < K && m < M) {
+  if (!whole && np < K) {
 #pragma unroll
     for (int r = 0; r < 8; r++) {
-      const int64_t nr = n + 8 * (r / 4) + r % 4;
-      if (nr >= N) continue;
+      const int64_t nr = row(r), mr = col(r);
+      if (nr >= N || mr >= M) continue;
       const float *xr = X.p + boff(X, b) + nr * X.sf;
-      const float *wr = W.p + boff(W, b) + m * W.sf;
+      const float *wr = W.p + boff(W, b) + mr * W.sf;
       float sumf = v[r];
       if (tail == kTailPinned) {
         for (int64_t k = np; k < K; k++) {
@@ -399,22 +400,29 @@ __device__ __forceinline__ void dot_store_rows(const MfmaOperand &X, const MfmaO
     }
   }
   if (ep.n > 0) {
-    const int64_t mc = m < M ? m : M - 1;
     epi_apply_n(ep, v, [&](const EpiOp &o, int r) {
-      const int64_t nr = n + 8 * (r / 4) + r % 4;
-      return b * o.s0 + (nr < N ? nr : N - 1) * o.s1 + mc * o.s2;
+      const int64_t nr = row(r), mr = col(r);
+      return b * o.s0 + (nr < N ? nr : N - 1) * o.s1 + (mr < M ? mr : M - 1) * o.s2;
     });
   }
-  float *y = Y + (b * N + n) * M + m;
+  float *y = Y + b * N * M;
   if (whole) {
 #pragma unroll
-    for (int r = 0; r < 8; r++) y[(8 * (r / 4) + r % 4) * M] = v[r];
+    for (int r = 0; r < 8; r++) y[row(r) * M + col(r)] = v[r];
     return;
   }
-  if (m >= M) return;
 #pragma unroll
   for (int r = 0; r < 8; r++)
-    if (n + 8 * (r / 4) + r % 4 < N) y[(8 * (r / 4) + r % 4) * M] = v[r];
+    if (row(r) < N && col(r) < M) y[row(r) * M + col(r)] = v[r];
+}
+
+// The 32x32 layout's 8 outputs per lane: rows n + 8 (r / 4) + r % 4 of column m.
+__device__ __forceinline__ void dot_store_rows(const MfmaOperand &X, const MfmaOperand &W, int64_t b, int64_t n,
+                                               int64_t m, int64_t N, int64_t M, int64_t K, int64_t np, int tail,
+                                               bool whole, const float (&out)[8], const Epilogue &ep,
+                                               float *__restrict__ Y) {
+  dot_store8(X, W, b, N, M, K, np, tail, whole, out, ep, Y, [&](int r) { return n + 8 * (r / 4) + r % 4; },
+             [&](int) { return m; });
 }
 
 template <int LX, int LW>
@@ -543,39 +551,58 @@ struct TileWalk {
   int tiles_n, tiles_m, db, dnt, dmt;
 };
 
+// ---- the 16x16 layout: every chain of an output in one lane -------------------------
+//
+// v_mfma_f32_16x16x1_4b_f32 adds one product to each output of four 16x16
+// blocks: lane l supplies A of block l/16 row l%16 and B of block l/16
+// column l%16, and block b's output (i, j) sits in lane j + 16 (i/4),
+// register 4b + i%4 (checked bit for bit against fmaf, as the 32x32 one).
+// A lane reads one float4 along k (k 16 blk + 4 (l/16) ..), so in the four
+// instructions g = 0..3 of a block, block b carries residue 4b + g: the 16
+// chains of an output (i, j) are the 16 (b, g) values of one lane, and the
+// ggml tree runs in registers with no exchange between waves.  A wave owns
+// 16 rows x 32 columns (two column blocks, 8 accumulator sets, 128 registers);
+// per block it reads one float4 of the lhs and two of the rhs and issues 8
+// instructions.  The LDS layout, the loaders and the stage schedule are
+// dot_mfma8_k's; the epilogue needs neither LDS nor a barrier.
+//
 // Persistent form: one workgroup per CU walks output tiles t = blockIdx.x,
 // blockIdx.x + gridDim.x, ..., and its stage pipeline runs straight across
 // tile boundaries, so the next tile's loads and LDS writes overlap this
 // tile's last stage and epilogue (a tile with K = 64 has one short stage).
-// The epilogue's exchange uses the stage buffer the tile's last stage read
-// from: the stage barrier ends its reads, the next tile's first stage went to
-// the other buffer, and the barrier after the epilogue keeps the next stage's
-// LDS writes out of it until the exchange has been read.  Tiles run
-// round-robin, so the workgroups that share an rhs tile at one time sit on one
-// XCD (for 4 row tiles per rhs tile).
-// The chains split by residue pairs: the rh = 0 wave holds (r, r + 8) for r
-// in {0, 1, 4, 5} and the rh = 1 wave r in {2, 3, 6, 7}; each finishes
-// w_r = (a[r] + a[r+8]) + (a[r+4] + a[r+12]) for two r of GGML_F32x4_REDUCE and
-// adds its pair, (w0 + w1) or (w2 + w3), so one value per output crosses for
-// vaddvq_f32's (w0 + w1) + (w2 + w3), and each wave half finishes and stores
-// half of the rows.  A block takes two float2 of each operand (k 16 b + 8 h +
-// 2 rh and + 4).  The smaller exchange pays where the epilogue is a large
-// share of a tile (short K); dot_mfma8_k's float4 reads where it is not.
+// Tiles run round-robin, so the workgroups that share an rhs tile at one time
+// sit on one XCD (for 4 row tiles per rhs tile).
+// Against the 32x32 layout in the same persistent form (the chains split
+// between two waves, one value per output exchanged through LDS between two
+// more barriers) attention went from 0.128 to 0.123 ms and the denoiser from
+// 6.50 to 6.39 ms.  Long contractions keep one workgroup per tile
+// (dot_mfma8_k): config 3 ran 5.44 ms persistent in this layout, 5.37
+// persistent in the 32x32 one, 5.16 per tile.
+typedef float v16f __attribute__((ext_vector_type(16)));
+
+__device__ __forceinline__ void mfma16_block(v16f (&acc)[2][4], const float4 &x, const float4 &w0, const float4 &w1,
+                                             bool first) {
+  const v16f z = {};
+  const float xv[4] = {x.x, x.y, x.z, x.w}, w0v[4] = {w0.x, w0.y, w0.z, w0.w}, w1v[4] = {w1.x, w1.y, w1.z, w1.w};
+#pragma unroll
+  for (int g = 0; g < 4; g++) {
+    acc[0][g] = __builtin_amdgcn_mfma_f32_16x16x1f32(xv[g], w0v[g], first ? z : acc[0][g], 0, 0, 0);
+    acc[1][g] = __builtin_amdgcn_mfma_f32_16x16x1f32(xv[g], w1v[g], first ? z : acc[1][g], 0, 0, 0);
+  }
+}
+
 template <int LX, int LW>
-__global__ void __launch_bounds__(512) dot_mfma8p_k(MfmaOperand X, MfmaOperand W, int64_t N, int64_t M, int64_t K,
-                                                    int tail, TileWalk tw, Epilogue ep, float *__restrict__ Y) {
+__global__ void __launch_bounds__(512) dot_mfma16p_k(MfmaOperand X, MfmaOperand W, int64_t N, int64_t M, int64_t K,
+                                                     int tail, TileWalk tw, Epilogue ep, float *__restrict__ Y) {
   constexpr int TH = 512, R = regs_of<TH>();
   extern __shared__ float lds_m[];  // [buffer][operand][kMT * kLS]
   auto tile = [&](int buf, int op) { return lds_m + (buf * 2 + op) * (kMT * kLS); };
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int quad = wave & 3, rh = wave >> 2;
-  const int wn = quad >> 1, wm = quad & 1;
-  const int h = lane >> 5, li = lane & 31;
+  const int wr = wave >> 1, wc = wave & 1;  // rows 16 wr .., columns 32 wc ..
+  const int l16 = lane & 15, kq = lane >> 4;
   const int64_t np = K & ~(int64_t)15;
   const int nb = (int)(np / 16);
   const int nst = (nb + kKC / 16 - 1) / (kKC / 16);
-  // Tile t = (b * tiles_n + nt) * tiles_m + mt; t advances by gridDim.x, whose
-  // digits in that mixed radix the host passes (no division per tile).
   int64_t t = blockIdx.x;  // the host launches at most `tiles` workgroups
   const int tiles_b = tw.tiles_n * tw.tiles_m;
   int b = (int)blockIdx.x / tiles_b, nt = ((int)blockIdx.x % tiles_b) / tw.tiles_m, mt = (int)blockIdx.x % tw.tiles_m;
@@ -591,13 +618,15 @@ __global__ void __launch_bounds__(512) dot_mfma8p_k(MfmaOperand X, MfmaOperand W
   }
   __syncthreads();
   int buf = 0;
-  v32f acc[4];
+  v16f acc[2][4];
   for (;;) {
     if (nst == 0) {  // K < 16: no block; the tail starts from the +0 tree
 #pragma unroll
-      for (int q = 0; q < 4; q++)
+      for (int c = 0; c < 2; c++)
 #pragma unroll
-        for (int r = 0; r < 32; r++) acc[q][r] = 0.0f;
+        for (int g = 0; g < 4; g++)
+#pragma unroll
+          for (int r = 0; r < 16; r++) acc[c][g][r] = 0.0f;
     }
     const int64_t tn = t + gridDim.x;
     const bool has_next = tn < tw.tiles;
@@ -608,27 +637,24 @@ __global__ void __launch_bounds__(512) dot_mfma8p_k(MfmaOperand X, MfmaOperand W
     const int64_t nn0 = has_next ? (int64_t)nt_ * kMT : n0, nm0 = has_next ? (int64_t)mt_ * kMT : m0;
     const BufOp nbx = buf_op<LX>(X, nb_, nn0), nbw = buf_op<LW>(W, nb_, nm0);
     for (int s = 0; s < nst; s++) {
-      const float *xs = tile(buf, 0) + (wn * 32 + li) * kLS + 8 * h + 2 * rh;
-      const float *ws = tile(buf, 1) + (wm * 32 + li) * kLS + 8 * h + 2 * rh;
+      const float *xs = tile(buf, 0) + (wr * 16 + l16) * kLS + 4 * kq;
+      const float *ws = tile(buf, 1) + (wc * 32 + l16) * kLS + 4 * kq;
       const int blocks = min(kKC / 16, nb - s * (kKC / 16));
-      // The next stage: this tile's s + 1, or the next tile's first.
       const bool here = s + 1 < nst;
       const bool more = here || has_next;
       const int fs = here ? s + 1 : 0;
       const int64_t fn0 = here ? n0 : nn0, fm0 = here ? m0 : nm0;
       const BufOp &fbx = here ? bx : nbx;
       const BufOp &fbw = here ? bw : nbw;
-      // As in dot_mfma8_k: straight-line blocks, block blk + 1's operands read
-      // (volatile, ahead of a scheduling barrier) before block blk's
+      // dot_mfma8_k's schedule: straight-line blocks, block blk + 1's operands
+      // read (volatile, ahead of a scheduling barrier) before block blk's
       // instructions issue; the next stage's loads after blocks 0 and 1, its
       // LDS writes after blocks 4 and 5.
-      auto rd = [&](int k, float4 &x, float4 &w) {
+      auto rd = [&](int k, float4 &x, float4 &w0, float4 &w1) {
         const int o = 16 * (k < blocks ? k : blocks - 1);  // blocks >= 1 in every stage
-        // (x.x, x.y, x.z, x.w) = residues 2 rh, 2 rh + 1, 2 rh + 4, 2 rh + 5
-        const float2 xl = ld2_lds_v(xs + o), xh = ld2_lds_v(xs + o + 4);
-        const float2 wl = ld2_lds_v(ws + o), wh = ld2_lds_v(ws + o + 4);
-        x = make_float4(xl.x, xl.y, xh.x, xh.y);
-        w = make_float4(wl.x, wl.y, wh.x, wh.y);
+        x = ld4_lds_v(xs + o);
+        w0 = ld4_lds_v(ws + o);
+        w1 = ld4_lds_v(ws + 16 * kLS + o);
       };
       auto part = [&](int q) {
         if (more) {
@@ -639,50 +665,41 @@ __global__ void __launch_bounds__(512) dot_mfma8p_k(MfmaOperand X, MfmaOperand W
         }
         __builtin_amdgcn_sched_barrier(0);
       };
-      float4 pa, qa, pb, qb;  // set p: even blocks, set q: odd blocks
-      rd(0, pa, qa);
+      float4 pa, pa0, pa1, pb, pb0, pb1;  // set p: even blocks, set q: odd blocks
+      rd(0, pa, pa0, pa1);
 #pragma unroll
       for (int blk = 0; blk < kKC / 16; blk += 2) {
-        rd(blk + 1, pb, qb);
+        rd(blk + 1, pb, pb0, pb1);
         __builtin_amdgcn_sched_barrier(0);
-        if (blk == 0 && s == 0) mfma_block4_first(acc, pa, qa);
-        else if (blk < blocks) mfma_block4(acc, pa, qa);
+        if (blk == 0 && s == 0) mfma16_block(acc, pa, pa0, pa1, true);
+        else if (blk < blocks) mfma16_block(acc, pa, pa0, pa1, false);
         if (blk == 0 || blk == 4) part(blk);
-        if (blk + 2 < kKC / 16) rd(blk + 2, pa, qa);
+        if (blk + 2 < kKC / 16) rd(blk + 2, pa, pa0, pa1);
         __builtin_amdgcn_sched_barrier(0);
-        if (blk + 1 < blocks) mfma_block4(acc, pb, qb);
+        if (blk + 1 < blocks) mfma16_block(acc, pb, pb0, pb1, false);
         if (blk == 0 || blk == 4) part(blk + 1);
       }
       __syncthreads();
       buf ^= 1;
     }
 
-    // Epilogue: register r of set q holds block r/16 of output row
-    // i = 8*((r%16)/4) + 4*h + r%4, column j = lane%32.  Wave half rh finishes
-    // rows r in [8 rh, 8 rh + 8) and hands the other half its pair sums for
-    // the rest, through the free stage buffer ([r % 8][lane] per wave).
-    float pw[16];
-#pragma unroll
-    for (int r = 0; r < 16; r++) {
-      float t4[4];
-#pragma unroll
-      for (int q = 0; q < 4; q++) t4[q] = acc[q][r] + acc[q][r + 16];  // sum[0]+=sum[2] / sum[1]+=sum[3]
-      pw[r] = (t4[0] + t4[2]) + (t4[1] + t4[3]);  // sum[0]+=sum[1] for two lanes, then their pair
-    }
-    float *give = tile(buf ^ 1, 0) + wave * (8 * 64);
-    const float *take = tile(buf ^ 1, 0) + (wave ^ 4) * (8 * 64);
-#pragma unroll
-    for (int r = 0; r < 8; r++) give[r * 64 + lane] = rh ? pw[r] : pw[8 + r];
-    __syncthreads();
+    // Epilogue: output (row 4 kq + ii, column 16 c + l16) of the wave's region
+    // holds residue 4b + g in register 4b + ii of set [c][g]: GGML_F32x4_REDUCE
+    // lane g is (a[g] + a[8+g]) + (a[4+g] + a[12+g]), then vaddvq_f32.
     float out[8];
 #pragma unroll
-    for (int r = 0; r < 8; r++) {
-      const float mine = rh ? pw[8 + r] : pw[r], other = take[r * 64 + lane];
-      out[r] = rh ? other + mine : mine + other;  // (w0 + w1) + (w2 + w3)
-    }
-    dot_store_rows(X, W, b, n0 + wn * 32 + 4 * h + 16 * rh, m0 + wm * 32 + li, N, M, K, np, tail,
-                   np == K && n0 + kMT <= N && m0 + kMT <= M, out, ep, Y);
-    __syncthreads();  // the exchange's buffer takes the stage after next's LDS writes
+    for (int c = 0; c < 2; c++)
+#pragma unroll
+      for (int ii = 0; ii < 4; ii++) {
+        float s4[4];
+#pragma unroll
+        for (int g = 0; g < 4; g++)
+          s4[g] = (acc[c][g][ii] + acc[c][g][8 + ii]) + (acc[c][g][4 + ii] + acc[c][g][12 + ii]);
+        out[4 * c + ii] = (s4[0] + s4[1]) + (s4[2] + s4[3]);
+      }
+    const int64_t nbase = n0 + wr * 16 + 4 * kq, mbase = m0 + wc * 32 + l16;
+    dot_store8(X, W, b, N, M, K, np, tail, np == K && n0 + kMT <= N && m0 + kMT <= M, out, ep, Y,
+               [&](int r) { return nbase + r % 4; }, [&](int r) { return mbase + 16 * (r / 4); });
     if (!has_next) break;
     t = tn;
     b = b_;
@@ -696,7 +713,6 @@ __global__ void __launch_bounds__(512) dot_mfma8p_k(MfmaOperand X, MfmaOperand W
 }
 
 constexpr int kDotLds = 2 * 2 * kMT * kLS * (int)sizeof(float);  // 135,168 bytes
-static_assert(8 * 8 * 64 <= 2 * kMT * kLS, "the persistent epilogue's exchange fits one stage buffer");
 static_assert(8 * 8 * 4 * 64 <= 4 * kMT * kLS, "dot_mfma8_k's epilogue exchange fits the LDS");
 constexpr int64_t kPersistStages = 4;
 
@@ -1421,7 +1437,7 @@ ArrayP dot_ggml(const DotOperand &lhs, const DotOperand &rhs, int64_t B, int64_t
     }
     static const bool lds_ok = [] {  // 135 KB of dynamic LDS, above the 64 KB default
 #define DOT_ATTR(a, c)                                                                                       \
-  SHLO_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(&dot_mfma8p_k<a, c>),                        \
+  SHLO_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(&dot_mfma16p_k<a, c>),                       \
                                hipFuncAttributeMaxDynamicSharedMemorySize, kDotLds));                       \
   SHLO_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(&dot_mfma8_k<a, c>),                         \
                                hipFuncAttributeMaxDynamicSharedMemorySize, kDotLds));
@@ -1443,10 +1459,9 @@ ArrayP dot_ggml(const DotOperand &lhs, const DotOperand &rhs, int64_t B, int64_t
     const int tiles_m = (int)tiles_m64;
     const int64_t tiles_b = tiles_n64 * tiles_m64, tiles = B * tiles_b;
     // Short contractions (up to kPersistStages stages of 128) run the
-    // persistent kernel with the one-value exchange, whose next tile's loads
-    // hide under this tile's epilogue (attention 0.173 ms against 0.189 one
-    // workgroup per tile); long ones one workgroup per tile (config 3,
-    // K = 4096: 5.21 ms against 5.36 persistent).
+    // persistent 16x16-layout kernel, whose next tile's loads hide under this
+    // tile's epilogue; long ones one workgroup per tile (config 3, K = 4096:
+    // 5.16 ms against 5.44 persistent).
     const int64_t stages = (K / 16 + kKC / 16 - 1) / (kKC / 16);
     const bool persist = stages <= kPersistStages;
     const unsigned grid = (unsigned)std::min<int64_t>(tiles, device_props().multiProcessorCount);  // one per CU
@@ -1459,7 +1474,7 @@ ArrayP dot_ggml(const DotOperand &lhs, const DotOperand &rhs, int64_t B, int64_t
       (void)kl, (void)kr, (void)ek;
 #define DOT_CASE(a, c)                                                                    \
   if (lx == a && lw == c) {                                                               \
-    if (persist) dot_mfma8p_k<a, c><<<grid, 512, kDotLds, s>>>(X, W, N, M, K, tl, tw, ep, Y);           \
+    if (persist) dot_mfma16p_k<a, c><<<grid, 512, kDotLds, s>>>(X, W, N, M, K, tl, tw, ep, Y);           \
     else dot_mfma8_k<a, c><<<grid1, 512, kDotLds, s>>>(X, W, N, M, K, tl, tiles_m, ep, Y);                  \
     return;                                                                               \
   }
