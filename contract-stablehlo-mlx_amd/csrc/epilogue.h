@@ -75,21 +75,22 @@ __device__ __forceinline__ void epi_op(float (&v)[NV], const float (&w)[NV], uin
 }
 
 // The same in two steps, for a producer that can issue the operand loads
-// long before its values are ready: epi_load_n, then epi_ops_n.
-template <int NV, class Off>
-__device__ __forceinline__ void epi_load_n(const Epilogue &e, float (&w)[kMaxEpi][NV], Off off) {
+// long before its values are ready: epi_load_n, then epi_ops_n, for the first
+// NE ops (epi_apply_n's `from` then takes the rest).
+template <int NE, int NV, class Off>
+__device__ __forceinline__ void epi_load_n(const Epilogue &e, float (&w)[NE][NV], Off off) {
 #pragma unroll
-  for (int k = 0; k < kMaxEpi; k++) {
+  for (int k = 0; k < NE; k++) {
     if (k >= e.n) break;
 #pragma unroll
     for (int r = 0; r < NV; r++) w[k][r] = e.op[k].p[off(e.op[k], r)];
   }
 }
 
-template <int NV>
-__device__ __forceinline__ void epi_ops_n(const Epilogue &e, float (&v)[NV], const float (&w)[kMaxEpi][NV]) {
+template <int NE, int NV>
+__device__ __forceinline__ void epi_ops_n(const Epilogue &e, float (&v)[NV], const float (&w)[NE][NV]) {
 #pragma unroll
-  for (int k = 0; k < kMaxEpi; k++) {
+  for (int k = 0; k < NE; k++) {
     if (k >= e.n) break;
     const EpiOp &o = e.op[k];
     switch (o.code) {
@@ -105,9 +106,10 @@ __device__ __forceinline__ void epi_ops_n(const Epilogue &e, float (&v)[NV], con
 }
 
 template <int NV, class Off>
-__device__ __forceinline__ void epi_apply_n(const Epilogue &e, float (&v)[NV], Off off) {
+__device__ __forceinline__ void epi_apply_n(const Epilogue &e, float (&v)[NV], Off off, int from = 0) {
 #pragma unroll
   for (int k = 0; k < kMaxEpi; k++) {
+    if (k < from) continue;
     if (k >= e.n) break;
     const EpiOp &o = e.op[k];
     float w[NV];

@@ -362,15 +362,35 @@ __device__ __forceinline__ void mfma_block4_first(v32f (&acc)[4], const float4 &
   acc[3] = __builtin_amdgcn_mfma_f32_32x32x1f32(a.w, b.w, z, 0, 0, 0);
 }
 
+// The fused ops whose operands the matrix kernels load before the products
+// (16 registers), so their latency hides under the tile's instructions.
+constexpr int kEpiEarly = 2;
+
+// Element offset of output (row, col)'s operand of a fused op, the indices
+// clamped into range (a discarded output reads a valid element).
+template <class RowF, class ColF>
+__device__ __forceinline__ int64_t dot_epi_off(const EpiOp &o, int64_t b, int64_t N, int64_t M, int r, RowF row,
+                                               ColF col) {
+  const int64_t nr = row(r), mr = col(r);
+  return b * o.s0 + (nr < N ? nr : N - 1) * o.s1 + (mr < M ? mr : M - 1) * o.s2;
+}
+
+template <class RowF, class ColF>
+__device__ __forceinline__ void dot_epi_early(const Epilogue &ep, int64_t b, int64_t N, int64_t M,
+                                              float (&pre)[kEpiEarly][8], RowF row, ColF col) {
+  epi_load_n(ep, pre, [&](const EpiOp &o, int r) { return dot_epi_off(o, b, N, M, r, row, col); });
+}
+
 // Stores the 8 outputs a lane finishes, output r at row row(r) and column
 // col(r), after the serial tail of dot_finish when K % 16 != 0 and the fused
-// element-wise ops.  `whole` (wave-uniform) says every output is in range and
+// element-wise ops (the first kEpiEarly with operands `pre` loaded by
+// dot_epi_early).  `whole` (wave-uniform) says every output is in range and
 // there is no tail.
 template <class RowF, class ColF>
 __device__ __forceinline__ void dot_store8(const MfmaOperand &X, const MfmaOperand &W, int64_t b, int64_t N,
                                            int64_t M, int64_t K, int64_t np, int tail, bool whole,
-                                           const float (&out)[8], const Epilogue &ep, float *__restrict__ Y, RowF row,
-                                           ColF col) {
+                                           const float (&out)[8], const Epilogue &ep, const float (&pre)[kEpiEarly][8],
+                                           float *__restrict__ Y, RowF row, ColF col) {
   float v[8];
 #pragma unroll
   for (int r = 0; r < 8; r++) v[r] = out[r];
@@ -400,10 +420,8 @@ __device__ __forceinline__ void dot_store8(const MfmaOperand &X, const MfmaOpera
     }
   }
   if (ep.n > 0) {
-    epi_apply_n(ep, v, [&](const EpiOp &o, int r) {
-      const int64_t nr = row(r), mr = col(r);
-      return b * o.s0 + (nr < N ? nr : N - 1) * o.s1 + (mr < M ? mr : M - 1) * o.s2;
-    });
+    epi_ops_n(ep, v, pre);
+    epi_apply_n(ep, v, [&](const EpiOp &o, int r) { return dot_epi_off(o, b, N, M, r, row, col); }, kEpiEarly);
   }
   float *y = Y + b * N * M;
   if (whole) {
@@ -416,14 +434,6 @@ __device__ __forceinline__ void dot_store8(const MfmaOperand &X, const MfmaOpera
     if (row(r) < N && col(r) < M) y[row(r) * M + col(r)] = v[r];
 }
 
-// The 32x32 layout's 8 outputs per lane: rows n + 8 (r / 4) + r % 4 of column m.
-__device__ __forceinline__ void dot_store_rows(const MfmaOperand &X, const MfmaOperand &W, int64_t b, int64_t n,
-                                               int64_t m, int64_t N, int64_t M, int64_t K, int64_t np, int tail,
-                                               bool whole, const float (&out)[8], const Epilogue &ep,
-                                               float *__restrict__ Y) {
-  dot_store8(X, W, b, N, M, K, np, tail, whole, out, ep, Y, [&](int r) { return n + 8 * (r / 4) + r % 4; },
-             [&](int) { return m; });
-}
 
 template <int LX, int LW>
 __global__ void __launch_bounds__(512) dot_mfma8_k(MfmaOperand X, MfmaOperand W, int64_t N, int64_t M, int64_t K,
@@ -447,6 +457,13 @@ __global__ void __launch_bounds__(512) dot_mfma8_k(MfmaOperand X, MfmaOperand W,
 #pragma unroll
       for (int r = 0; r < 32; r++) acc[q][r] = 0.0f;
   }
+
+  // This lane's 8 outputs: rows nl + 8 (r / 4) + r % 4 of column ml.
+  const int64_t nl = n0 + wn * 32 + 4 * (lane >> 5) + 16 * rh, ml = m0 + wm * 32 + (lane & 31);
+  auto orow = [&](int r) { return nl + 8 * (r / 4) + r % 4; };
+  auto ocol = [&](int) { return ml; };
+  float pre[kEpiEarly][8];
+  dot_epi_early(ep, b, N, M, pre, orow, ocol);
 
   float4 rx[R], rw[R];
   const BufOp bx = buf_op<LX>(X, b, n0), bw = buf_op<LW>(W, b, m0);
@@ -532,16 +549,9 @@ __global__ void __launch_bounds__(512) dot_mfma8_k(MfmaOperand X, MfmaOperand W,
     }
     out[r] = (w[0] + w[1]) + (w[2] + w[3]);  // vaddvq_f32
   }
-  dot_store_rows(X, W, b, n0 + wn * 32 + 4 * h + 16 * rh, m0 + wm * 32 + li, N, M, K, np, tail,
-                 np == K && n0 + kMT <= N && m0 + kMT <= M, out, ep, Y);
+  dot_store8(X, W, b, N, M, K, np, tail, np == K && n0 + kMT <= N && m0 + kMT <= M, out, ep, pre, Y, orow, ocol);
 }
 
-typedef float f32x2 __attribute__((ext_vector_type(2)));
-typedef const volatile __attribute__((address_space(3))) f32x2 lds_f32x2;
-__device__ __forceinline__ float2 ld2_lds_v(const float *p) {
-  const f32x2 v = *(lds_f32x2 *)(p);
-  return make_float2(v.x, v.y);
-}
 
 // The persistent kernel's tile walk: tiles (b, nt, mt) in row-major order over
 // (B, tiles_n, tiles_m), and gridDim.x = (db * tiles_n + dnt) * tiles_m + dmt
@@ -636,6 +646,12 @@ __global__ void __launch_bounds__(512) dot_mfma16p_k(MfmaOperand X, MfmaOperand 
     const int nb_ = has_next ? b_ : b;
     const int64_t nn0 = has_next ? (int64_t)nt_ * kMT : n0, nm0 = has_next ? (int64_t)mt_ * kMT : m0;
     const BufOp nbx = buf_op<LX>(X, nb_, nn0), nbw = buf_op<LW>(W, nb_, nm0);
+    // This lane's 8 outputs: rows nbase + r % 4 of columns mbase + 16 (r / 4).
+    const int64_t nbase = n0 + wr * 16 + 4 * kq, mbase = m0 + wc * 32 + l16;
+    auto orow = [&](int r) { return nbase + r % 4; };
+    auto ocol = [&](int r) { return mbase + 16 * (r / 4); };
+    float pre[kEpiEarly][8];
+    dot_epi_early(ep, b, N, M, pre, orow, ocol);
     for (int s = 0; s < nst; s++) {
       const float *xs = tile(buf, 0) + (wr * 16 + l16) * kLS + 4 * kq;
       const float *ws = tile(buf, 1) + (wc * 32 + l16) * kLS + 4 * kq;
@@ -697,9 +713,8 @@ __global__ void __launch_bounds__(512) dot_mfma16p_k(MfmaOperand X, MfmaOperand 
           s4[g] = (acc[c][g][ii] + acc[c][g][8 + ii]) + (acc[c][g][4 + ii] + acc[c][g][12 + ii]);
         out[4 * c + ii] = (s4[0] + s4[1]) + (s4[2] + s4[3]);
       }
-    const int64_t nbase = n0 + wr * 16 + 4 * kq, mbase = m0 + wc * 32 + l16;
-    dot_store8(X, W, b, N, M, K, np, tail, np == K && n0 + kMT <= N && m0 + kMT <= M, out, ep, Y,
-               [&](int r) { return nbase + r % 4; }, [&](int r) { return mbase + 16 * (r / 4); });
+    dot_store8(X, W, b, N, M, K, np, tail, np == K && n0 + kMT <= N && m0 + kMT <= M, out, ep, pre, Y, orow,
+               ocol);
     if (!has_next) break;
     t = tn;
     b = b_;
