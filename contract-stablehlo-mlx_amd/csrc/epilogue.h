@@ -39,9 +39,11 @@ __host__ __device__ inline float f32_binary(uint32_t op, float x, float y) {
   }
 }
 
-// Up to kMaxEpi binary ops applied in order to an output value v at index
-// (i0, i1, i2) of the producer's output: v = op(v, p[i0*s0 + i1*s1 + i2*s2]),
-// or op(p[...], v) when `rev` (the produced value was the op's right operand).
+// Up to kMaxEpi ops applied in order to an output value v at index
+// (i0, i1, i2) of the producer's output: a binary op v = op(v, p[i0*s0 +
+// i1*s1 + i2*s2]), or op(p[...], v) when `rev` (the produced value was the
+// op's right operand); or the unary ggml gelu_erf (code kEpiGeluErf, no
+// operand; the producer supplies the routine).
 struct EpiOp {
   const float *p;
   int64_t s0, s1, s2;
@@ -50,13 +52,25 @@ struct EpiOp {
 struct Epilogue {
   EpiOp op[kMaxEpi];
   int n = 0;
+  int gelu = 0;  // some op is kEpiGeluErf
 };
 
-__device__ __forceinline__ float epi_apply(const Epilogue &e, float v, int64_t i0, int64_t i1, int64_t i2) {
+// The identity for producers whose chains hold no unary op.
+struct NoUnary {
+  __device__ float operator()(float v) const { return v; }
+};
+
+template <class Unary = NoUnary>
+__device__ __forceinline__ float epi_apply(const Epilogue &e, float v, int64_t i0, int64_t i1, int64_t i2,
+                                           Unary un = Unary()) {
 #pragma unroll
   for (int k = 0; k < kMaxEpi; k++) {
     if (k < e.n) {
       const EpiOp &o = e.op[k];
+      if (o.code == kEpiGeluErf) {
+        v = un(v);
+        continue;
+      }
       const float w = o.p[i0 * o.s0 + i1 * o.s1 + i2 * o.s2];
       v = o.rev ? f32_binary(o.code, w, v) : f32_binary(o.code, v, w);
     }
@@ -82,18 +96,25 @@ __device__ __forceinline__ void epi_load_n(const Epilogue &e, float (&w)[NE][NV]
 #pragma unroll
   for (int k = 0; k < NE; k++) {
     if (k >= e.n) break;
+    if (e.op[k].code == kEpiGeluErf) continue;
 #pragma unroll
     for (int r = 0; r < NV; r++) w[k][r] = e.op[k].p[off(e.op[k], r)];
   }
 }
 
-template <int NE, int NV>
-__device__ __forceinline__ void epi_ops_n(const Epilogue &e, float (&v)[NV], const float (&w)[NE][NV]) {
+
+template <int NE, int NV, class Unary = NoUnary>
+__device__ __forceinline__ void epi_ops_n(const Epilogue &e, float (&v)[NV], const float (&w)[NE][NV],
+                                          Unary un = Unary()) {
 #pragma unroll
   for (int k = 0; k < NE; k++) {
     if (k >= e.n) break;
     const EpiOp &o = e.op[k];
     switch (o.code) {
+      case kEpiGeluErf:
+#pragma unroll
+        for (int r = 0; r < NV; r++) v[r] = un(v[r]);
+        break;
       case kAdd: epi_op<kAdd>(v, w[k], o.rev); break;
       case kSub: epi_op<kSub>(v, w[k], o.rev); break;
       case kMul: epi_op<kMul>(v, w[k], o.rev); break;
@@ -105,13 +126,19 @@ __device__ __forceinline__ void epi_ops_n(const Epilogue &e, float (&v)[NV], con
   }
 }
 
-template <int NV, class Off>
-__device__ __forceinline__ void epi_apply_n(const Epilogue &e, float (&v)[NV], Off off, int from = 0) {
+template <int NV, class Off, class Unary = NoUnary>
+__device__ __forceinline__ void epi_apply_n(const Epilogue &e, float (&v)[NV], Off off, int from = 0,
+                                            Unary un = Unary()) {
 #pragma unroll
   for (int k = 0; k < kMaxEpi; k++) {
     if (k < from) continue;
     if (k >= e.n) break;
     const EpiOp &o = e.op[k];
+    if (o.code == kEpiGeluErf) {
+#pragma unroll
+      for (int r = 0; r < NV; r++) v[r] = un(v[r]);
+      continue;
+    }
     float w[NV];
 #pragma unroll
     for (int r = 0; r < NV; r++) w[r] = o.p[off(o, r)];

@@ -47,6 +47,41 @@ __device__ __forceinline__ void st4_nt(float *p, float4 v) {
 }
 
 
+// ---- gelu_erf's per-element routine (also a fused epilogue op of dot_general) ----------
+
+constexpr int kPolyWords = erffk::kTab * 6;
+
+// Stages the coefficient table in LDS (16-byte loads; the table is read from
+// L2 after the first blocks).
+__device__ __forceinline__ void load_poly(double *tab) {
+  const double2 *src = reinterpret_cast<const double2 *>(&erffk::kPoly[0][0]);
+  for (int i = threadIdx.x; i < kPolyWords / 2; i += blockDim.x) reinterpret_cast<double2 *>(tab)[i] = src[i];
+  __syncthreads();
+}
+
+template <int TANH>
+__device__ __forceinline__ float gelu1(float x, const double *tab) {
+  float ev;
+  if (TANH)  // planted: the tanh form of GELU (Shaders.lean:192-194)
+    ev = tanhf(bits_f(0x3F4C422Au) * x * (1.0f + bits_f(0x3D372713u) * x * x));
+  else
+    ev = erffk::erff_cr(x * bits_f(0x3F3504F3u), tab);  // SQRT_2_INV
+  float y = (0.5f * x) * (1.0f + ev);
+  // A NaN input gives the input quieted, payload kept (Shaders.lean:196-199).
+  if ((f_bits(x) & 0x7FFFFFFFu) > 0x7F800000u) y = bits_f(f_bits(x) | 0x00400000u);
+  return y;
+}
+
+// Four elements at once, the same results as gelu1 element by element.
+//
+// 64 |x*SQRT_2_INV| is taken as one product |x| * (64*SQRT_2_INV) (the
+// scaling is exact), clamped to 255: the same value wherever x*SQRT_2_INV is
+// a normal binary32, and where it is subnormal (|x| < 1.7e-38) erf of it is
+// below 2^-125, so 1 + ev rounds to 1 either way.  The four erf evaluations
+// share one (rarely taken) branch into the exception table, keyed by
+// |x*SQRT_2_INV|.  NaN inputs need no select: the clamp maps them to erf = 1,
+// ev = +-1, and (0.5f*x)*(1 + ev) multiplies the quieted x, payload kept, by
+// 2 or 0, which returns it.
 // ---- dot_general in ggml_vec_dot_f32 order --------------------------------------
 
 // The tail and the final combination shared by every dot kernel: `a` holds the
@@ -104,6 +139,9 @@ template <int TAIL>
 __global__ void __launch_bounds__(256) dot_ggml_simple(int64_t n_out, int64_t N, int64_t M, int64_t K,
                                                        MfmaOperand X, MfmaOperand W, Epilogue ep,
                                                        float *__restrict__ y) {
+  __shared__ double gtab[kPolyWords];  // a fused gelu_erf's table
+  if (ep.gelu) load_poly(gtab);
+  auto gelu = [&](float x) { return gelu1<0>(x, gtab); };
   const int64_t lk = X.sk, rk = W.sk;
   for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n_out; i += (int64_t)gridDim.x * blockDim.x) {
     const int64_t m = i % M, t = i / M, n = t % N, b = t / N;
@@ -115,7 +153,7 @@ __global__ void __launch_bounds__(256) dot_ggml_simple(int64_t n_out, int64_t N,
         const float p = w[k * rk] * x[k * lk];
         s = s + p;
       }
-      y[i] = epi_apply(ep, s, b, n, m);
+      y[i] = epi_apply(ep, s, b, n, m, gelu);
       continue;
     }
     float a[16];
@@ -126,7 +164,7 @@ __global__ void __launch_bounds__(256) dot_ggml_simple(int64_t n_out, int64_t N,
 #pragma unroll
       for (int j = 0; j < 16; j++) a[j] = __builtin_fmaf(w[(k0 + j) * rk], x[(k0 + j) * lk], a[j]);
     }
-    y[i] = epi_apply(ep, dot_finish<TAIL>(a, w, rk, x, lk, np, K), b, n, m);
+    y[i] = epi_apply(ep, dot_finish<TAIL>(a, w, rk, x, lk, np, K), b, n, m, gelu);
   }
 }
 
@@ -154,6 +192,7 @@ typedef float v32f __attribute__((ext_vector_type(32)));
 constexpr int kMT = 64;        // tile rows (n) and columns (m)
 constexpr int kKC = 128;       // k per stage (8 blocks of 16)
 constexpr int kLS = kKC + 4;   // LDS row stride (floats): rows start 4 banks apart
+constexpr int kDotStageFloats = 2 * 2 * kMT * kLS;  // two buffers of both operands; a fused gelu_erf's table follows
 // float4 per thread per operand per stage for a workgroup of TH threads.
 template <int TH>
 constexpr int regs_of() {
@@ -390,7 +429,7 @@ template <class RowF, class ColF>
 __device__ __forceinline__ void dot_store8(const MfmaOperand &X, const MfmaOperand &W, int64_t b, int64_t N,
                                            int64_t M, int64_t K, int64_t np, int tail, bool whole,
                                            const float (&out)[8], const Epilogue &ep, const float (&pre)[kEpiEarly][8],
-                                           float *__restrict__ Y, RowF row, ColF col) {
+                                           const double *gtab, float *__restrict__ Y, RowF row, ColF col) {
   float v[8];
 #pragma unroll
   for (int r = 0; r < 8; r++) v[r] = out[r];
@@ -420,8 +459,10 @@ __device__ __forceinline__ void dot_store8(const MfmaOperand &X, const MfmaOpera
     }
   }
   if (ep.n > 0) {
-    epi_ops_n(ep, v, pre);
-    epi_apply_n(ep, v, [&](const EpiOp &o, int r) { return dot_epi_off(o, b, N, M, r, row, col); }, kEpiEarly);
+    auto gelu = [&](float x) { return gelu1<0>(x, gtab); };
+    epi_ops_n(ep, v, pre, gelu);
+    epi_apply_n(
+        ep, v, [&](const EpiOp &o, int r) { return dot_epi_off(o, b, N, M, r, row, col); }, kEpiEarly, gelu);
   }
   float *y = Y + b * N * M;
   if (whole) {
@@ -464,6 +505,8 @@ __global__ void __launch_bounds__(512) dot_mfma8_k(MfmaOperand X, MfmaOperand W,
   auto ocol = [&](int) { return ml; };
   float pre[kEpiEarly][8];
   dot_epi_early(ep, b, N, M, pre, orow, ocol);
+  double *gtab = reinterpret_cast<double *>(lds_m + kDotStageFloats);  // a fused gelu_erf's table
+  if (ep.gelu) load_poly(gtab);
 
   float4 rx[R], rw[R];
   const BufOp bx = buf_op<LX>(X, b, n0), bw = buf_op<LW>(W, b, m0);
@@ -549,7 +592,8 @@ __global__ void __launch_bounds__(512) dot_mfma8_k(MfmaOperand X, MfmaOperand W,
     }
     out[r] = (w[0] + w[1]) + (w[2] + w[3]);  // vaddvq_f32
   }
-  dot_store8(X, W, b, N, M, K, np, tail, np == K && n0 + kMT <= N && m0 + kMT <= M, out, ep, pre, Y, orow, ocol);
+  dot_store8(X, W, b, N, M, K, np, tail, np == K && n0 + kMT <= N && m0 + kMT <= M, out, ep, pre, gtab, Y, orow,
+             ocol);
 }
 
 
@@ -618,6 +662,8 @@ __global__ void __launch_bounds__(512) dot_mfma16p_k(MfmaOperand X, MfmaOperand 
   int b = (int)blockIdx.x / tiles_b, nt = ((int)blockIdx.x % tiles_b) / tw.tiles_m, mt = (int)blockIdx.x % tw.tiles_m;
   int64_t n0 = (int64_t)nt * kMT, m0 = (int64_t)mt * kMT;
   BufOp bx = buf_op<LX>(X, b, n0), bw = buf_op<LW>(W, b, m0);
+  double *gtab = reinterpret_cast<double *>(lds_m + kDotStageFloats);  // a fused gelu_erf's table
+  if (ep.gelu) load_poly(gtab);
 
   float4 rx[R], rw[R];
   if (nst > 0) {
@@ -713,8 +759,8 @@ __global__ void __launch_bounds__(512) dot_mfma16p_k(MfmaOperand X, MfmaOperand 
           s4[g] = (acc[c][g][ii] + acc[c][g][8 + ii]) + (acc[c][g][4 + ii] + acc[c][g][12 + ii]);
         out[4 * c + ii] = (s4[0] + s4[1]) + (s4[2] + s4[3]);
       }
-    dot_store8(X, W, b, N, M, K, np, tail, np == K && n0 + kMT <= N && m0 + kMT <= M, out, ep, pre, Y, orow,
-               ocol);
+    dot_store8(X, W, b, N, M, K, np, tail, np == K && n0 + kMT <= N && m0 + kMT <= M, out, ep, pre, gtab, Y,
+               orow, ocol);
     if (!has_next) break;
     t = tn;
     b = b_;
@@ -727,7 +773,9 @@ __global__ void __launch_bounds__(512) dot_mfma16p_k(MfmaOperand X, MfmaOperand 
   }
 }
 
-constexpr int kDotLds = 2 * 2 * kMT * kLS * (int)sizeof(float);  // 135,168 bytes
+constexpr int kDotLds = kDotStageFloats * (int)sizeof(float);                     // 135,168 bytes
+constexpr int kDotLdsGelu = kDotLds + kPolyWords * (int)sizeof(double);            // 147,456 bytes
+static_assert(kDotStageFloats % 4 == 0, "the gelu table starts 16-byte aligned");
 static_assert(8 * 8 * 4 * 64 <= 4 * kMT * kLS, "dot_mfma8_k's epilogue exchange fits the LDS");
 constexpr int64_t kPersistStages = 4;
 
@@ -1270,39 +1318,6 @@ __global__ void __launch_bounds__(256) silu_k(int64_t n, int64_t cols, int gpu_o
 
 // ---- gelu_erf and the erff map ------------------------------------------------------
 
-constexpr int kPolyWords = erffk::kTab * 6;
-
-// Stages the coefficient table in LDS (16-byte loads; the table is read from
-// L2 after the first blocks).
-__device__ __forceinline__ void load_poly(double *tab) {
-  const double2 *src = reinterpret_cast<const double2 *>(&erffk::kPoly[0][0]);
-  for (int i = threadIdx.x; i < kPolyWords / 2; i += blockDim.x) reinterpret_cast<double2 *>(tab)[i] = src[i];
-  __syncthreads();
-}
-
-template <int TANH>
-__device__ __forceinline__ float gelu1(float x, const double *tab) {
-  float ev;
-  if (TANH)  // planted: the tanh form of GELU (Shaders.lean:192-194)
-    ev = tanhf(bits_f(0x3F4C422Au) * x * (1.0f + bits_f(0x3D372713u) * x * x));
-  else
-    ev = erffk::erff_cr(x * bits_f(0x3F3504F3u), tab);  // SQRT_2_INV
-  float y = (0.5f * x) * (1.0f + ev);
-  // A NaN input gives the input quieted, payload kept (Shaders.lean:196-199).
-  if ((f_bits(x) & 0x7FFFFFFFu) > 0x7F800000u) y = bits_f(f_bits(x) | 0x00400000u);
-  return y;
-}
-
-// Four elements at once, the same results as gelu1 element by element.
-//
-// 64 |x*SQRT_2_INV| is taken as one product |x| * (64*SQRT_2_INV) (the
-// scaling is exact), clamped to 255: the same value wherever x*SQRT_2_INV is
-// a normal binary32, and where it is subnormal (|x| < 1.7e-38) erf of it is
-// below 2^-125, so 1 + ev rounds to 1 either way.  The four erf evaluations
-// share one (rarely taken) branch into the exception table, keyed by
-// |x*SQRT_2_INV|.  NaN inputs need no select: the clamp maps them to erf = 1,
-// ev = +-1, and (0.5f*x)*(1 + ev) multiplies the quieted x, payload kept, by
-// 2 or 0, which returns it.
 template <int TANH>
 __device__ __forceinline__ float4 gelu4(float4 v, const double *tab) {
   if (TANH) return make_float4(gelu1<1>(v.x, tab), gelu1<1>(v.y, tab), gelu1<1>(v.z, tab), gelu1<1>(v.w, tab));
@@ -1402,6 +1417,11 @@ Epilogue make_epilogue(const std::vector<FusedOp> &ops, std::vector<ArrayP> *kee
   if (ops.size() > (size_t)kMaxEpi) fail(strf("fused epilogue: at most %d ops", kMaxEpi));
   Epilogue ep;
   for (const FusedOp &o : ops) {
+    if (o.code == kEpiGeluErf) {
+      ep.op[ep.n++] = EpiOp{nullptr, 0, 0, 0, o.code, 0u};
+      ep.gelu = 1;
+      continue;
+    }
     if (!o.arr || o.arr->dtype != kF32 || !o.arr->buf) fail("fused epilogue: f32 operands only");
     ep.op[ep.n++] = EpiOp{(const float *)o.arr->data(), o.s0, o.s1, o.s2, o.code, o.rev ? 1u : 0u};
     keep->push_back(o.arr);
@@ -1453,9 +1473,9 @@ ArrayP dot_ggml(const DotOperand &lhs, const DotOperand &rhs, int64_t B, int64_t
     static const bool lds_ok = [] {  // 135 KB of dynamic LDS, above the 64 KB default
 #define DOT_ATTR(a, c)                                                                                       \
   SHLO_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(&dot_mfma16p_k<a, c>),                       \
-                               hipFuncAttributeMaxDynamicSharedMemorySize, kDotLds));                       \
+                               hipFuncAttributeMaxDynamicSharedMemorySize, kDotLdsGelu));                       \
   SHLO_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(&dot_mfma8_k<a, c>),                         \
-                               hipFuncAttributeMaxDynamicSharedMemorySize, kDotLds));
+                               hipFuncAttributeMaxDynamicSharedMemorySize, kDotLdsGelu));
       DOT_ATTR(kLoadRowVec, kLoadRowVec) DOT_ATTR(kLoadRowVec, kLoadColVec) DOT_ATTR(kLoadRowVec, kLoadScalar)
       DOT_ATTR(kLoadColVec, kLoadRowVec) DOT_ATTR(kLoadColVec, kLoadColVec) DOT_ATTR(kLoadColVec, kLoadScalar)
       DOT_ATTR(kLoadScalar, kLoadRowVec) DOT_ATTR(kLoadScalar, kLoadColVec) DOT_ATTR(kLoadScalar, kLoadScalar)
@@ -1479,6 +1499,7 @@ ArrayP dot_ggml(const DotOperand &lhs, const DotOperand &rhs, int64_t B, int64_t
     // 5.16 ms against 5.44 persistent).
     const int64_t stages = (K / 16 + kKC / 16 - 1) / (kKC / 16);
     const bool persist = stages <= kPersistStages;
+    const unsigned lds = ep.gelu ? kDotLdsGelu : kDotLds;
     const unsigned grid = (unsigned)std::min<int64_t>(tiles, device_props().multiProcessorCount);  // one per CU
     TileWalk tw{tiles, (int)tiles_n64, tiles_m, (int)(grid / tiles_b), (int)((grid % tiles_b) / tiles_m64),
                 (int)(grid % tiles_m64)};
@@ -1489,8 +1510,8 @@ ArrayP dot_ggml(const DotOperand &lhs, const DotOperand &rhs, int64_t B, int64_t
       (void)kl, (void)kr, (void)ek;
 #define DOT_CASE(a, c)                                                                    \
   if (lx == a && lw == c) {                                                               \
-    if (persist) dot_mfma16p_k<a, c><<<grid, 512, kDotLds, s>>>(X, W, N, M, K, tl, tw, ep, Y);           \
-    else dot_mfma8_k<a, c><<<grid1, 512, kDotLds, s>>>(X, W, N, M, K, tl, tiles_m, ep, Y);                  \
+    if (persist) dot_mfma16p_k<a, c><<<grid, 512, lds, s>>>(X, W, N, M, K, tl, tw, ep, Y);               \
+    else dot_mfma8_k<a, c><<<grid1, 512, lds, s>>>(X, W, N, M, K, tl, tiles_m, ep, Y);                      \
     return;                                                                               \
   }
       DOT_CASE(kLoadRowVec, kLoadRowVec) DOT_CASE(kLoadRowVec, kLoadColVec) DOT_CASE(kLoadRowVec, kLoadScalar)
@@ -1612,6 +1633,8 @@ ArrayP norm(const ArrayP &x0, int64_t rows, int64_t cols, uint32_t eps_bits, boo
   if (rows * cols != x0->size()) fail("ggml.norm: rows*cols is not the element count");
   if (cols > 4096) fail("ggml.norm: rows above 4096 columns are not carried");
   if (gpu_ops && !epi.empty()) fail("ggml.norm: no fused ops with the planted binary32 sums");
+  for (const FusedOp &o : epi)
+    if (o.code == kEpiGeluErf) fail("ggml.norm: gelu_erf is not a fused op of norm");
   ArrayP x = contiguous(x0);
   auto y = new_array(kF32, x->shape);
   if (rows == 0 || cols == 0) return y;

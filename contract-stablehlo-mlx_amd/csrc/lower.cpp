@@ -221,17 +221,21 @@ DotOperand dot_operand(const ArrayP &a, const std::vector<int64_t> &batch, const
 }
 
 // An element-wise op that follows a producer: `other` is its second operand,
-// `rev` says the produced value is its right operand.
+// `rev` says the produced value is its right operand; code kEpiGeluErf is
+// ggml.gelu_erf (no operand).
 struct Chained {
   uint32_t code;
   bool rev;
   ArrayP other;
 };
 
-// Applies the chain's ops from `from` on as separate element-wise kernels.
+// Applies the chain's ops from `from` on as separate kernels.
 ArrayP apply_chain(ArrayP v, const std::vector<Chained> &chain, size_t from) {
-  for (size_t i = from; i < chain.size(); i++)
-    v = chain[i].rev ? binary(chain[i].code, chain[i].other, v) : binary(chain[i].code, v, chain[i].other);
+  for (size_t i = from; i < chain.size(); i++) {
+    const Chained &c = chain[i];
+    if (c.code == kEpiGeluErf) v = reshape(gelu_erf(v, false), v->shape);
+    else v = c.rev ? binary(c.code, c.other, v) : binary(c.code, v, c.other);
+  }
   return v;
 }
 
@@ -239,10 +243,18 @@ ArrayP apply_chain(ArrayP v, const std::vector<Chained> &chain, size_t from) {
 // the dim groups g0, g1, g2 of `dims` can fuse: each other operand f32 of
 // shape `dims`, its strides flat over every group.
 std::vector<FusedOp> fusable_prefix(const std::vector<Chained> &chain, const Shape &dims,
-                                    const std::vector<int64_t> (&g)[3]) {
+                                    const std::vector<int64_t> (&g)[3], bool gelu_ok) {
   std::vector<FusedOp> out;
   for (const Chained &c : chain) {
-    if ((int)out.size() == kMaxEpi || c.other->dtype != kF32 || c.other->shape != dims || !c.other->buf) break;
+    if ((int)out.size() == kMaxEpi) break;
+    if (c.code == kEpiGeluErf) {
+      if (!gelu_ok) break;
+      FusedOp op;
+      op.code = kEpiGeluErf;
+      out.push_back(op);
+      continue;
+    }
+    if (c.other->dtype != kF32 || c.other->shape != dims || !c.other->buf) break;
     FusedOp op;
     if (!flat_stride(c.other, g[0], &op.s0) || !flat_stride(c.other, g[1], &op.s1) ||
         !flat_stride(c.other, g[2], &op.s2))
@@ -309,7 +321,7 @@ ArrayP dot_general(const Faults &f, const Op &o, const ArrayP &a, const ArrayP &
   std::vector<int64_t> g[3];
   const size_t nb = lb.size(), nl = lf.size();
   for (size_t d = 0; d < out.dims.size(); d++) g[d < nb ? 0 : d < nb + nl ? 1 : 2].push_back((int64_t)d);
-  const std::vector<FusedOp> epi = fusable_prefix(chain, out.dims, g);
+  const std::vector<FusedOp> epi = fusable_prefix(chain, out.dims, g, true);
   ArrayP y = dot_ggml(L, R, B, N, M, K, f.dot_plain ? (int)kTailPlain : default_dot_tail(), epi);
   return apply_chain(reshape(y, out.dims), chain, epi.size());
 }
@@ -571,7 +583,7 @@ struct Lowerer {
     std::vector<int64_t> g[3];
     for (size_t d = 0; d < out.dims.size(); d++) g[d + 1 < out.dims.size() ? 1 : 2].push_back((int64_t)d);
     const bool can = !f.norm_gpu_ops && rc.second <= 4 * 64 * kNormEpiJ;
-    const std::vector<FusedOp> epi = can ? fusable_prefix(chain, out.dims, g) : std::vector<FusedOp>{};
+    const std::vector<FusedOp> epi = can ? fusable_prefix(chain, out.dims, g, false) : std::vector<FusedOp>{};
     ArrayP y = norm(x, rc.first, rc.second, f32_attr(attrs, "eps"), f.norm_gpu_ops, epi);
     return apply_chain(reshape(y, out.dims), chain, epi.size());
   }
@@ -624,6 +636,14 @@ struct Lowerer {
   // Whether `e` can take the value `cur` of type `vt` into a fused chain;
   // *other = the index of its other operand.
   bool chainable(const Op &e, const Ty &vt, const std::string &cur, int *other) const {
+    if ((e.name == "stablehlo.custom_call" || e.name == "stablehlo.composite") &&
+        composite_name(e) == "ggml.gelu_erf") {  // unary: any operand count but one is refused
+      if (f.gelu_tanh || e.operands.size() != 1 || e.operands[0] != cur || e.results.size() != 1 ||
+          e.out_tys.size() != 1 || e.out_tys[0].el != "f32" || e.out_tys[0].dims != vt.dims)
+        return false;
+      *other = -1;
+      return true;
+    }
     if (f.binary_half) return false;  // planted: binary ops through f16
     uint32_t c = 0;
     const bool div = e.name == "stablehlo.divide" && !f.divide_builtin;
@@ -693,6 +713,11 @@ struct Lowerer {
     std::vector<Chained> chain;
     for (int k : ch) {
       const Op &e = ops[k];
+      if (e.operands.size() == 1) {  // ggml.gelu_erf
+        chain.push_back(Chained{kEpiGeluErf, false, nullptr});
+        cur = e.results[0];
+        continue;
+      }
       const bool rev = e.operands[1] == cur;
       uint32_t c = kDiv;
       if (e.name != "stablehlo.divide") binary_code(e.name, &c);

@@ -79,6 +79,7 @@ struct DotOperand {
 // (op(o, v) when `rev`), o the element of `arr` at i0*s0 + i1*s1 + i2*s2 for
 // the producer's output index (i0, i1, i2).  Same bits as the separate op.
 constexpr int kMaxEpi = 4;  // fused ops per producer
+constexpr uint32_t kEpiGeluErf = 0x100;  // FusedOp code of ggml gelu_erf (no operand)
 struct FusedOp {
   ArrayP arr;  // f32; keeps the buffer alive
   int64_t s0 = 0, s1 = 0, s2 = 0;

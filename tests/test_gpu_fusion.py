@@ -77,6 +77,12 @@ class Chain:
         cur = "%v0"
         names = ["%v0"]
         for i, (name, arg, how, rev) in enumerate(self.ops):
+            if name == "gelu":  # ggml.gelu_erf, no operand
+                lines.append(f'    %v{i + 1} = "stablehlo.custom_call"({cur}) {{call_target_name = "ggml.gelu_erf", '
+                             f'backend_config = ""}} : ({t(o)}) -> {t(o)}\n')
+                cur = f"%v{i + 1}"
+                names.append(cur)
+                continue
             args.append(f"%x{i}: {t(arg.shape)}")
             other = f"%x{i}"
             if how is not None and how[0] == "bcast":
@@ -108,6 +114,10 @@ class Chain:
         vals = [v]
         o = self.out_shape
         for name, arg, how, rev in self.ops:
+            if name == "gelu":
+                v = oracle.gelu_erf(np.ascontiguousarray(v, F32)).reshape(o)
+                vals.append(v)
+                continue
             if how is None:
                 other = arg
             elif how[0] == "bcast":
@@ -138,7 +148,7 @@ def check(oracle, ch, seed=5, flavors=(0, 1)):
     a_sh = ch.batch + (ch.N, ch.K)
     b_sh = ch.batch + ((ch.M, ch.K) if ch.rhs_mk else (ch.K, ch.M))
     a, b = normal(oracle, seed, a_sh), normal(oracle, seed + 1, b_sh)
-    ins = [a, b] + [arg for _, arg, _, _ in ch.ops]
+    ins = [a, b] + [arg for name, arg, _, _ in ch.ops if name != "gelu"]
     text = ch.module()
     for flavor in flavors:
         want = ch.expect(oracle, a, b, flavor)
@@ -265,3 +275,39 @@ def test_planted_faults_still_differ(oracle):
     for fault in ("dot_plain", "dot_builtin", "binary_half", "divide_builtin", "broadcast_first"):
         got = run(text, ins, faults=shlo_hip.fault_bits(fault))[0]
         assert not same_bits(got, want), fault
+
+
+@pytest.mark.parametrize("N,K,M", [(256, 512, 192), (130, 1024, 70), (33, 33, 9), (64, 16, 64)])
+def test_bias_then_gelu(oracle, N, K, M):
+    """x W + bias, then ggml.gelu_erf (the FFN's first projection): the
+    correctly rounded erff runs in the product's epilogue from a table in LDS;
+    the persistent kernel, the per-tile kernel, partial tiles and tails."""
+    bias = normal(oracle, 60, (M,), 0.5)
+    check(oracle, Chain((), N, K, M, [("add", bias, ("bcast", (1,)), False), ("gelu", None, None, False)]))
+
+
+def test_gelu_inside_a_chain(oracle):
+    """gelu_erf between binary ops, special values in the operands."""
+    N, K, M = 96, 64, 96
+    res = normal(oracle, 61, (N, M), 3.0)
+    res.reshape(-1)[::17] = np.nan
+    res.reshape(-1)[1::19] = np.inf
+    ops = [("multiply", scalar(4.0), ("bcast", ()), False), ("gelu", None, None, False),
+           ("add", res, None, True), ("gelu", None, None, False)]
+    check(oracle, Chain((), N, K, M, ops))
+
+
+def test_gelu_with_many_batches(oracle):
+    """More than 65535 batches: the one-thread-per-output kernel's table."""
+    B, N, K, M = 70000, 1, 20, 2
+    check(oracle, Chain((B,), N, K, M, [("gelu", None, None, False)]), flavors=(0,))
+
+
+def test_planted_gelu_fault_still_differs(oracle):
+    import shlo_hip
+    N, K, M = 64, 64, 64
+    ch = Chain((), N, K, M, [("add", normal(oracle, 62, (M,)), ("bcast", (1,)), False), ("gelu", None, None, False)])
+    text, ins = check(oracle, ch, flavors=(0,))
+    want = ch.expect(oracle, ins[0], ins[1], 0)[0]
+    got = run(text, ins, faults=shlo_hip.fault_bits("gelu_tanh"))[0]
+    assert not same_bits(got, want)
