@@ -862,6 +862,12 @@ __device__ __forceinline__ int row16_min(int v) {
   v = min(v, dpp_i<kDppHalfMirror>(v));
   return min(v, dpp_i<kDppMirror>(v));
 }
+// Whole-wave binary64 sum and int minimum, the same on every lane: rows of 16
+// through DPP, then the four row results read as scalars and added as
+// (r0 + r1) + (r2 + r3).  Six levels, as a butterfly over 64 lanes; the
+// callers' error bounds count only the depth.
+__device__ __forceinline__ double wave_sum_d(double v);
+__device__ __forceinline__ int wave_min_i(int v);
 __device__ __forceinline__ float lane_f(float v, int l) {
   return bits_f((uint32_t)__builtin_amdgcn_readlane((int)f_bits(v), l));
 }
@@ -870,6 +876,22 @@ __device__ __forceinline__ double lane_d(double v, int l) {
   const uint32_t lo = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)u, l);
   const uint32_t hi = (uint32_t)__builtin_amdgcn_readlane((int)(uint32_t)(u >> 32), l);
   return __builtin_bit_cast(double, ((uint64_t)hi << 32) | lo);
+}
+__device__ __forceinline__ double wave_sum_d(double v) {
+  v = row16_sum(v);
+  return (lane_d(v, 0) + lane_d(v, 16)) + (lane_d(v, 32) + lane_d(v, 48));
+}
+__device__ __forceinline__ float wave_max_f(float v) {
+  v = __builtin_fmaxf(v, bits_f((uint32_t)dpp_i<kDppXor1>((int)f_bits(v))));
+  v = __builtin_fmaxf(v, bits_f((uint32_t)dpp_i<kDppXor2>((int)f_bits(v))));
+  v = __builtin_fmaxf(v, bits_f((uint32_t)dpp_i<kDppHalfMirror>((int)f_bits(v))));
+  v = __builtin_fmaxf(v, bits_f((uint32_t)dpp_i<kDppMirror>((int)f_bits(v))));
+  return __builtin_fmaxf(__builtin_fmaxf(lane_f(v, 0), lane_f(v, 16)), __builtin_fmaxf(lane_f(v, 32), lane_f(v, 48)));
+}
+__device__ __forceinline__ int wave_min_i(int v) {
+  v = row16_min(v);
+  return min(min(__builtin_amdgcn_readlane(v, 0), __builtin_amdgcn_readlane(v, 16)),
+             min(__builtin_amdgcn_readlane(v, 32), __builtin_amdgcn_readlane(v, 48)));
 }
 
 // fin(S) for the in-order binary64 sum S of a row's parts: group part
@@ -890,11 +912,8 @@ __device__ __forceinline__ float ordered_sum_apply(const float (&part)[J], int G
     ls = ls + (double)tail;
     le = min(le, part_ulp_exp(tail));
   }
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    ls = ls + __shfl_xor(ls, o, kWave);
-    le = min(le, __shfl_xor(le, o, kWave));
-  }
+  ls = wave_sum_d(ls);
+  le = wave_min_i(le);
   if (ls <= exact_limit(le)) return fin(ls);
   const double d = ls * 0x1p-40;  // exact: ls >= 2^-149 or ls = 0
   const float f_lo = fin(ls - d), f_hi = fin(ls + d);
@@ -982,8 +1001,7 @@ __global__ void __launch_bounds__(256) soft_max_rows_k(int64_t rows, int cols, f
       mx = __builtin_fmaxf(mx, __builtin_fmaxf(__builtin_fmaxf(e[j].x, e[j].y), __builtin_fmaxf(e[j].z, e[j].w)));
     }
   }
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) mx = __builtin_fmaxf(mx, __shfl_xor(mx, o, kWave));
+  mx = wave_max_f(mx);
   // The arguments x*sc - mx are <= 0 (or -inf, or NaN): the fast form, with
   // the rare 126 < |n| <= 192 elements recomputed when any lane has one.
   float4 v[J];
@@ -1178,7 +1196,7 @@ __global__ void __launch_bounds__(256) norm_rows_k(int64_t rows, int cols, float
   const float et = lane < T ? x[4 * G + lane] : 0.0f;
   // The fused ops' operands do not depend on the row's sums: their loads go
   // out now and land under the reductions.
-  float w[kMaxEpi][4 * J], wt[kMaxEpi][1];
+  float w[kEpiEarly][4 * J], wt[kEpiEarly][1];  // the first kEpiEarly ops' operands; later ops load at the end
   if (EPI) {
     epi_load_n(ep, w, [&](const EpiOp &o, int r) {
       const int g = lane + kWave * (r / 4);
@@ -1202,12 +1220,9 @@ __global__ void __launch_bounds__(256) norm_rows_k(int64_t rows, int cols, float
     take(e[j].w);
   }
   take(et);
-#pragma unroll
-  for (int o = 32; o > 0; o >>= 1) {
-    ls = ls + __shfl_xor(ls, o, kWave);
-    la = la + __shfl_xor(la, o, kWave);
-    le = min(le, __shfl_xor(le, o, kWave));
-  }
+  ls = wave_sum_d(ls);
+  la = wave_sum_d(la);
+  le = wave_min_i(le);
   const float fc = (float)cols;
   float mean;
   if (la <= exact_limit(le)) {
@@ -1276,8 +1291,18 @@ __global__ void __launch_bounds__(256) norm_rows_k(int64_t rows, int cols, float
   }
   float tv[1] = {dt * scl};
   if (EPI) {
+    auto off = [&](const EpiOp &o, int r) {
+      const int g = lane + kWave * (r / 4);
+      const int c = (FULL || g < G) ? 4 * g + r % 4 : 0;
+      return row * o.s1 + c * o.s2;
+    };
     epi_ops_n(ep, v, w);
-    if (T > 0) epi_ops_n(ep, tv, wt);
+    epi_apply_n(ep, v, off, kEpiEarly);
+    if (T > 0) {
+      epi_ops_n(ep, tv, wt);
+      epi_apply_n(ep, tv, [&](const EpiOp &o, int) { return row * o.s1 + (lane < T ? 4 * G + lane : 0) * o.s2; },
+                  kEpiEarly);
+    }
   }
   float *y = Y + row * cols;
 #pragma unroll
