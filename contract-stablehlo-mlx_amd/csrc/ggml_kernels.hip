@@ -597,6 +597,149 @@ __global__ void __launch_bounds__(512) dot_mfma8_k(MfmaOperand X, MfmaOperand W,
 }
 
 
+// ---- dot_mfma8_k with both operands loaded straight into LDS ----------------------
+//
+// For an lhs read along k and an rhs read along its free dim, every read in
+// range by construction (kLoadRowVecB, kLoadColQuadB): buffer_load_dwordx4 with
+// the lds bit writes each lane's 16 bytes to LDS at the instruction's LDS base
+// + 16 lane (checked on the device), so a stage needs no staging registers and
+// no LDS store instructions, and the next stage's loads go out at the start of
+// this stage, a whole stage before the barrier that waits for them.  One
+// instruction fills 1 KB of LDS contiguously, so rows are unpadded:
+//   lhs [64 rows][32 k-quads]: k-quad q of row r sits at chunk 32 r + (q ^ (r & 15)),
+//     so 16 consecutive rows reading one k-quad hit 16 distinct bank quads;
+//   rhs [128 k][16 m-quads] (the free dim contiguous, as in HBM): a lane reads
+//     its column one k at a time, 32 lanes on 32 consecutive floats.
+// The two stage buffers are separate LDS variables and the stage loop is
+// unrolled by two, so the buffer being filled and the one being read are
+// different objects to the compiler.  Chains, epilogue and stores are
+// dot_mfma8_k's.
+typedef __attribute__((address_space(3))) void lds_void;
+typedef const volatile __attribute__((address_space(3))) float lds_f32;
+__device__ __forceinline__ float ld1_lds_v(const float *p) { return *(lds_f32 *)(p); }
+
+template <int LX, int LW>
+__global__ void __launch_bounds__(512) dot_mfma8d_k(MfmaOperand X, MfmaOperand W, int64_t N, int64_t M, int64_t K,
+                                                    int tiles_m, Epilogue ep, float *__restrict__ Y) {
+  static_assert(LX == kLoadRowVecB && LW == kLoadColQuadB, "direct loads: lhs along k, rhs along its free dim");
+  constexpr int kChunks = kMT * kKC / 4;  // 16-byte chunks per operand per stage
+  __shared__ float4 dx0[kChunks], dx1[kChunks], dw0[kChunks], dw1[kChunks];
+  __shared__ double gtab[kPolyWords];  // a fused gelu_erf's table
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int quad = wave & 3, rh = wave >> 2;
+  const int wn = quad >> 1, wm = quad & 1;
+  const int64_t b = blockIdx.y;
+  const int64_t n0 = (int64_t)(blockIdx.x / tiles_m) * kMT, m0 = (int64_t)(blockIdx.x % tiles_m) * kMT;
+  const int nst = (int)(K / kKC);  // every stage full (the host checks)
+
+  const int64_t nl = n0 + wn * 32 + 4 * (lane >> 5) + 16 * rh, ml = m0 + wm * 32 + (lane & 31);
+  auto orow = [&](int r) { return nl + 8 * (r / 4) + r % 4; };
+  auto ocol = [&](int) { return ml; };
+  float pre[kEpiEarly][8];
+  dot_epi_early(ep, b, N, M, pre, orow, ocol);
+  if (ep.gelu) load_poly(gtab);
+
+  // Loads.  Instruction i (0..3) of wave w fills chunks 64 (8 i + w) .. + 63 of
+  // each operand: lhs rows 16 i + 2 w + lane / 32 (lane % 32 is the chunk's
+  // position in its row), rhs k rows 32 i + 4 w + lane / 16, m-quad lane % 16.
+  // The per-instruction and per-stage advances go in the scalar offset.
+  const int wv = __builtin_amdgcn_readfirstlane(wave);
+  const __amdgpu_buffer_rsrc_t bx =
+      __builtin_amdgcn_make_buffer_rsrc((void *)(X.p + boff(X, b)), (short)0, 0x7FFFFFFF, 0x00020000);
+  const __amdgpu_buffer_rsrc_t bw =
+      __builtin_amdgcn_make_buffer_rsrc((void *)(W.p + boff(W, b)), (short)0, 0x7FFFFFFF, 0x00020000);
+  const int xr = 2 * wave + lane / 32;  // row within each 16-row group
+  const int xvoff = (int)(((n0 + xr) * X.sf + 4 * ((lane % 32) ^ (xr & 15))) * 4);
+  const int wvoff = (int)((m0 + 4 * (lane % 16) + (int64_t)(4 * wave + lane / 16) * W.sk) * 4);
+  auto dma_x = [&](float4 *dx, int s) {
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(bx, (lds_void *)(dx + 64 * (8 * i + wv)), 16, xvoff,
+                                               (int)((16 * i * X.sf + (int64_t)kKC * s) * 4), 0, 0);
+  };
+  auto dma_w = [&](float4 *dw, int s) {
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(bw, (lds_void *)(dw + 64 * (8 * i + wv)), 16, wvoff,
+                                               (int)(((int64_t)32 * i + (int64_t)kKC * s) * W.sk * 4), 0, 0);
+  };
+
+  // Reads.  lhs: row wn 32 + li, k-quad 4 blk + 2 h + rh at chunk
+  // row 32 + 4 (blk ^ kh) + kx (kh, kx: the row key's high and low bits);
+  // rhs: float (16 blk + 8 h + 4 rh + q) 64 + wm 32 + li.
+  const int h = lane >> 5, li = lane & 31;
+  const int xrow = wn * 32 + li, key = xrow & 15;
+  const int kx = (2 * h + rh) ^ (key & 3), kh = key >> 2;
+  int xa[4];
+#pragma unroll
+  for (int j = 0; j < 4; j++) xa[j] = xrow * kKC + 4 * (4 * (j ^ kh) + kx);  // floats; block blk: xa[blk & 3] + 64 (blk >> 2)
+  const int wa = (8 * h + 4 * rh) * kMT + wm * 32 + li;
+
+  v32f acc[4];
+  auto stage = [&](const float4 *cx, const float4 *cw, float4 *nx, float4 *nw, int s) {
+    const float *xs = reinterpret_cast<const float *>(cx), *ws = reinterpret_cast<const float *>(cw);
+    const bool more = s + 1 < nst;
+    auto rd = [&](int k, float4 &x, float4 &w) {
+      x = ld4_lds_v(xs + xa[k & 3] + 64 * (k >> 2));
+      const float *q = ws + wa + 16 * k * kMT;
+      w = make_float4(ld1_lds_v(q), ld1_lds_v(q + kMT), ld1_lds_v(q + 2 * kMT), ld1_lds_v(q + 3 * kMT));
+    };
+    float4 pa, qa, pb, qb;  // set p: even blocks, set q: odd blocks
+    rd(0, pa, qa);
+#pragma unroll
+    for (int blk = 0; blk < kKC / 16; blk += 2) {
+      rd(blk + 1, pb, qb);
+      __builtin_amdgcn_sched_barrier(0);
+      if (blk == 0 && s == 0) mfma_block4_first(acc, pa, qa);
+      else mfma_block4(acc, pa, qa);
+      if (blk == 0 && more) dma_x(nx, s + 1);
+      if (blk + 2 < kKC / 16) rd(blk + 2, pa, qa);
+      __builtin_amdgcn_sched_barrier(0);
+      mfma_block4(acc, pb, qb);
+      if (blk == 0 && more) dma_w(nw, s + 1);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    __builtin_amdgcn_s_waitcnt(0);  // this wave's loads have landed in LDS
+    __syncthreads();
+  };
+  dma_x(dx0, 0);
+  dma_w(dw0, 0);
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+  for (int s = 0; s < nst; s += 2) {
+    stage(dx0, dw0, dx1, dw1, s);
+    if (s + 1 < nst) stage(dx1, dw1, dx0, dw0, s + 1);
+  }
+
+  // Epilogue: dot_mfma8_k's, the exchange in the lhs buffers (waves 0..3 in
+  // dx0, 4..7 in dx1; no load is outstanding after the last stage).
+  float t4[16][4];
+#pragma unroll
+  for (int r = 0; r < 16; r++)
+#pragma unroll
+    for (int q = 0; q < 4; q++) t4[r][q] = acc[q][r] + acc[q][r + 16];
+  float *give = reinterpret_cast<float *>(rh ? dx1 : dx0) + quad * (8 * 4 * 64);  // [r % 8][q][lane]
+  const float *take = reinterpret_cast<const float *>(rh ? dx0 : dx1) + quad * (8 * 4 * 64);
+#pragma unroll
+  for (int r = 0; r < 8; r++)
+#pragma unroll
+    for (int q = 0; q < 4; q++) give[(r * 4 + q) * 64 + lane] = rh ? t4[r][q] : t4[8 + r][q];
+  __syncthreads();
+  float out[8];
+#pragma unroll
+  for (int r = 0; r < 8; r++) {
+    float w[4];
+#pragma unroll
+    for (int q = 0; q < 4; q++) {
+      const float mine = rh ? t4[8 + r][q] : t4[r][q], other = take[(r * 4 + q) * 64 + lane];
+      w[q] = rh ? other + mine : mine + other;  // sum[0] += sum[1]
+    }
+    out[r] = (w[0] + w[1]) + (w[2] + w[3]);  // vaddvq_f32
+  }
+  dot_store8(X, W, b, N, M, K, K, kTailStock, true, out, ep, pre, gtab, Y, orow, ocol);
+}
+
+
 // The persistent kernel's tile walk: tiles (b, nt, mt) in row-major order over
 // (B, tiles_n, tiles_m), and gridDim.x = (db * tiles_n + dnt) * tiles_m + dmt
 // with dnt < tiles_n, dmt < tiles_m.
@@ -1533,6 +1676,10 @@ ArrayP dot_ggml(const DotOperand &lhs, const DotOperand &rhs, int64_t B, int64_t
     const int tl = tail;
     launch([=](hipStream_t s) {
       (void)kl, (void)kr, (void)ek;
+      if (!persist && lx == kLoadRowVecB && lw == kLoadColQuadB) {  // both operands straight into LDS
+        dot_mfma8d_k<kLoadRowVecB, kLoadColQuadB><<<grid1, 512, 0, s>>>(X, W, N, M, K, tiles_m, ep, Y);
+        return;
+      }
 #define DOT_CASE(a, c)                                                                    \
   if (lx == a && lw == c) {                                                               \
     if (persist) dot_mfma16p_k<a, c><<<grid, 512, lds, s>>>(X, W, N, M, K, tl, tw, ep, Y);               \

@@ -123,6 +123,28 @@ def test_dot_many_tiles(oracle, B, N, M, K):
             shlo_hip.set_flavor(0)
 
 
+
+@pytest.mark.parametrize("B,N,M,K", [(2, 128, 192, 640), (1, 192, 128, 768), (3, 64, 64, 1152)])
+def test_dot_direct_lds_loads(oracle, B, N, M, K):
+    """Long contractions (more than four stages of 128) with the lhs read along
+    k, the rhs along its free dim and rows multiples of 64: both operands go
+    from HBM straight into LDS.  Odd and even stage counts (5, 6, 9), several
+    tiles and batches, both flavours, eager and compiled."""
+    import shlo_hip
+    lhs, st = oracle.fill_normal(37, 1.0, B * N * K)
+    rhs, _ = oracle.fill_normal(37, 1.0, B * K * M, state=st)
+    lhs, rhs = lhs.reshape(B, N, K), rhs.reshape(B, K, M)
+    for flavor in (0, 1):
+        want = oracle.dot_general_bnk(lhs, np.ascontiguousarray(rhs.transpose(0, 2, 1)), flavor)
+        shlo_hip.set_flavor(flavor)
+        try:
+            for compile in (True, False):
+                got = run(dot_module(N, K, M, batch=B), [lhs, rhs], compile=compile)[0]
+                assert same_bits(got, want), (flavor, compile)
+        finally:
+            shlo_hip.set_flavor(0)
+
+
 def causal_logits(oracle, rows, cols, sigma=4.0, seed=7):
     x, _ = oracle.fill_normal(seed, sigma, rows * cols)
     x = x.reshape(rows, cols)

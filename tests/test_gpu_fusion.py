@@ -277,7 +277,7 @@ def test_planted_faults_still_differ(oracle):
         assert not same_bits(got, want), fault
 
 
-@pytest.mark.parametrize("N,K,M", [(256, 512, 192), (130, 1024, 70), (33, 33, 9), (64, 16, 64)])
+@pytest.mark.parametrize("N,K,M", [(256, 512, 192), (130, 1024, 70), (128, 1024, 128), (33, 33, 9), (64, 16, 64)])
 def test_bias_then_gelu(oracle, N, K, M):
     """x W + bias, then ggml.gelu_erf (the FFN's first projection): the
     correctly rounded erff runs in the product's epilogue from a table in LDS;
