@@ -124,12 +124,15 @@ def test_dot_many_tiles(oracle, B, N, M, K):
 
 
 
-@pytest.mark.parametrize("B,N,M,K", [(2, 128, 192, 640), (1, 192, 128, 768), (3, 64, 64, 1152)])
+@pytest.mark.parametrize("B,N,M,K", [(2, 128, 192, 640), (1, 192, 128, 768), (3, 64, 64, 1152),
+                                     (5, 512, 512, 128), (3, 512, 704, 384), (1, 128, 64, 256)])
 def test_dot_direct_lds_loads(oracle, B, N, M, K):
-    """Long contractions (more than four stages of 128) with the lhs read along
-    k, the rhs along its free dim and rows multiples of 64: both operands go
-    from HBM straight into LDS.  Odd and even stage counts (5, 6, 9), several
-    tiles and batches, both flavours, eager and compiled."""
+    """Contractions in full stages of 128 with the lhs read along k, the rhs
+    along its free dim and rows multiples of 64: both operands go from HBM
+    straight into LDS.  Per-tile kernel with odd and even stage counts (5, 6,
+    9); persistent kernel walking more tiles than CUs with 1 and 3 stages per
+    tile (the stage buffers alternate across tile boundaries) and with 2.  Both
+    flavours, eager and compiled."""
     import shlo_hip
     lhs, st = oracle.fill_normal(37, 1.0, B * N * K)
     rhs, _ = oracle.fill_normal(37, 1.0, B * K * M, state=st)
