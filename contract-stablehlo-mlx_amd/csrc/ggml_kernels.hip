@@ -599,8 +599,8 @@ __global__ void __launch_bounds__(512) dot_mfma8_k(MfmaOperand X, MfmaOperand W,
 
 // ---- dot_mfma8_k with both operands loaded straight into LDS ----------------------
 //
-// For an lhs read along k and an rhs read along its free dim, every read in
-// range by construction (kLoadRowVecB, kLoadColQuadB): buffer_load_dwordx4 with
+// For an lhs read along k and an rhs read along its free dim or along k,
+// every read in range by construction: buffer_load_dwordx4 with
 // the lds bit writes each lane's 16 bytes to LDS at the instruction's LDS base
 // + 16 lane (checked on the device), so a stage needs no staging registers and
 // no LDS store instructions, and the next stage's loads go out at the start of
@@ -608,8 +608,13 @@ __global__ void __launch_bounds__(512) dot_mfma8_k(MfmaOperand X, MfmaOperand W,
 // instruction fills 1 KB of LDS contiguously, so rows are unpadded:
 //   lhs [64 rows][32 k-quads]: k-quad q of row r sits at chunk 32 r + (q ^ (r & 15)),
 //     so 16 consecutive rows reading one k-quad hit 16 distinct bank quads;
-//   rhs [128 k][16 m-quads] (the free dim contiguous, as in HBM): a lane reads
-//     its column one k at a time, 32 lanes on 32 consecutive floats.
+//   rhs along its free dim (LW = kLoadColQuadB): [KC k][16 m-quads], as in
+//     HBM: a lane reads its column one k at a time, 32 lanes on 32
+//     consecutive floats;
+//   rhs along k (LW = kLoadRowVecB): [64 columns][KC / 4 k-quads], swizzled
+//     and read as the lhs.
+// KC = 128 k per stage, or 64 for contractions in multiples of 64 (Q K^T
+// with K = 64: rows of 16 chunks, 4 rows per instruction).
 // The two stage buffers are separate LDS variables and the stage loop is
 // unrolled by two, so the buffer being filled and the one being read are
 // different objects to the compiler.  Chains, epilogue and stores are
@@ -618,11 +623,13 @@ typedef __attribute__((address_space(3))) void lds_void;
 typedef const volatile __attribute__((address_space(3))) float lds_f32;
 __device__ __forceinline__ float ld1_lds_v(const float *p) { return *(lds_f32 *)(p); }
 
-template <int LX, int LW>
+template <int LX, int LW, int KC>
 __global__ void __launch_bounds__(512) dot_mfma8d_k(MfmaOperand X, MfmaOperand W, int64_t N, int64_t M, int64_t K,
                                                     int tiles_m, Epilogue ep, float *__restrict__ Y) {
-  static_assert(LX == kLoadRowVecB && LW == kLoadColQuadB, "direct loads: lhs along k, rhs along its free dim");
-  constexpr int kChunks = kMT * kKC / 4;  // 16-byte chunks per operand per stage
+  static_assert(LX == kLoadRowVecB && (LW == kLoadColQuadB || LW == kLoadRowVecB), "direct loads: lhs along k");
+  static_assert(KC == 128 || KC == 64, "stages of 128 or 64 k");
+  constexpr int kChunks = kMT * kKC / 4;  // 16-byte chunks per buffer (a stage of KC = 64 uses half)
+  constexpr int CPR = KC / 4, RPI = 64 / CPR, NI = KC / 32;  // chunks per row, rows per instruction, instructions per wave
   __shared__ float4 dx0[kChunks], dx1[kChunks], dw0[kChunks], dw1[kChunks];
   __shared__ double gtab[kPolyWords];  // a fused gelu_erf's table
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
@@ -630,7 +637,7 @@ __global__ void __launch_bounds__(512) dot_mfma8d_k(MfmaOperand X, MfmaOperand W
   const int wn = quad >> 1, wm = quad & 1;
   const int64_t b = blockIdx.y;
   const int64_t n0 = (int64_t)(blockIdx.x / tiles_m) * kMT, m0 = (int64_t)(blockIdx.x % tiles_m) * kMT;
-  const int nst = (int)(K / kKC);  // every stage full (the host checks)
+  const int nst = (int)(K / KC);  // every stage full (the host checks)
 
   const int64_t nl = n0 + wn * 32 + 4 * (lane >> 5) + 16 * rh, ml = m0 + wm * 32 + (lane & 31);
   auto orow = [&](int r) { return nl + 8 * (r / 4) + r % 4; };
@@ -639,40 +646,50 @@ __global__ void __launch_bounds__(512) dot_mfma8d_k(MfmaOperand X, MfmaOperand W
   dot_epi_early(ep, b, N, M, pre, orow, ocol);
   if (ep.gelu) load_poly(gtab);
 
-  // Loads.  Instruction i (0..3) of wave w fills chunks 64 (8 i + w) .. + 63 of
-  // each operand: lhs rows 16 i + 2 w + lane / 32 (lane % 32 is the chunk's
-  // position in its row), rhs k rows 32 i + 4 w + lane / 16, m-quad lane % 16.
-  // The per-instruction and per-stage advances go in the scalar offset.
+  // Loads.  Instruction i (0..NI-1) of wave w fills chunks 64 (8 i + w) .. + 63
+  // of each operand: lhs rows RPI (8 i + w) + lane / CPR (lane % CPR is the
+  // chunk's position in its row; the swizzle key, row & 15, does not depend
+  // on i); a free-dim rhs k rows 32 i + 4 w + lane / 16, m-quad lane % 16; a
+  // k-contiguous rhs as the lhs.  The per-instruction and per-stage advances
+  // go in the scalar offset.
   const int wv = __builtin_amdgcn_readfirstlane(wave);
   const __amdgpu_buffer_rsrc_t bx =
       __builtin_amdgcn_make_buffer_rsrc((void *)(X.p + boff(X, b)), (short)0, 0x7FFFFFFF, 0x00020000);
   const __amdgpu_buffer_rsrc_t bw =
       __builtin_amdgcn_make_buffer_rsrc((void *)(W.p + boff(W, b)), (short)0, 0x7FFFFFFF, 0x00020000);
-  const int xr = 2 * wave + lane / 32;  // row within each 16-row group
-  const int xvoff = (int)(((n0 + xr) * X.sf + 4 * ((lane % 32) ^ (xr & 15))) * 4);
-  const int wvoff = (int)((m0 + 4 * (lane % 16) + (int64_t)(4 * wave + lane / 16) * W.sk) * 4);
+  const int xr = RPI * wave + lane / CPR;  // row of instruction 0
+  const int xvoff = (int)(((n0 + xr) * X.sf + 4 * ((lane % CPR) ^ (xr & 15))) * 4);
+  const int wvoff = LW == kLoadColQuadB
+                        ? (int)((m0 + 4 * (lane % 16) + (int64_t)(4 * wave + lane / 16) * W.sk) * 4)
+                        : (int)(((m0 + xr) * W.sf + 4 * ((lane % CPR) ^ (xr & 15))) * 4);
   auto dma_x = [&](float4 *dx, int s) {
 #pragma unroll
-    for (int i = 0; i < 4; i++)
+    for (int i = 0; i < NI; i++)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(bx, (lds_void *)(dx + 64 * (8 * i + wv)), 16, xvoff,
-                                               (int)((16 * i * X.sf + (int64_t)kKC * s) * 4), 0, 0);
+                                               (int)((8 * RPI * i * X.sf + (int64_t)KC * s) * 4), 0, 0);
   };
   auto dma_w = [&](float4 *dw, int s) {
 #pragma unroll
-    for (int i = 0; i < 4; i++)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(bw, (lds_void *)(dw + 64 * (8 * i + wv)), 16, wvoff,
-                                               (int)(((int64_t)32 * i + (int64_t)kKC * s) * W.sk * 4), 0, 0);
+    for (int i = 0; i < NI; i++) {
+      const int so = LW == kLoadColQuadB ? (int)(((int64_t)32 * i + (int64_t)KC * s) * W.sk * 4)
+                                         : (int)((8 * RPI * i * W.sf + (int64_t)KC * s) * 4);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(bw, (lds_void *)(dw + 64 * (8 * i + wv)), 16, wvoff, so, 0, 0);
+    }
   };
 
   // Reads.  lhs: row wn 32 + li, k-quad 4 blk + 2 h + rh at chunk
-  // row 32 + 4 (blk ^ kh) + kx (kh, kx: the row key's high and low bits);
-  // rhs: float (16 blk + 8 h + 4 rh + q) 64 + wm 32 + li.
+  // row CPR + 4 (blk ^ kh) + kx (kh, kx: the row key's high and low bits);
+  // a free-dim rhs: float (16 blk + 8 h + 4 rh + q) 64 + wm 32 + li; a
+  // k-contiguous rhs: column wm 32 + li as an lhs row (the same key).
   const int h = lane >> 5, li = lane & 31;
-  const int xrow = wn * 32 + li, key = xrow & 15;
+  const int key = li & 15;  // (wn 32 + li) & 15 and (wm 32 + li) & 15
   const int kx = (2 * h + rh) ^ (key & 3), kh = key >> 2;
-  int xa[4];
+  int xa[4], wa4[4];
 #pragma unroll
-  for (int j = 0; j < 4; j++) xa[j] = xrow * kKC + 4 * (4 * (j ^ kh) + kx);  // floats; block blk: xa[blk & 3] + 64 (blk >> 2)
+  for (int j = 0; j < 4; j++) {  // floats; block blk: xa[blk & 3] + 64 (blk >> 2)
+    xa[j] = (wn * 32 + li) * KC + 4 * (4 * (j ^ kh) + kx);
+    wa4[j] = (wm * 32 + li) * KC + 4 * (4 * (j ^ kh) + kx);
+  }
   const int wa = (8 * h + 4 * rh) * kMT + wm * 32 + li;
 
   v32f acc[4];
@@ -681,19 +698,23 @@ __global__ void __launch_bounds__(512) dot_mfma8d_k(MfmaOperand X, MfmaOperand W
     const bool more = s + 1 < nst;
     auto rd = [&](int k, float4 &x, float4 &w) {
       x = ld4_lds_v(xs + xa[k & 3] + 64 * (k >> 2));
-      const float *q = ws + wa + 16 * k * kMT;
-      w = make_float4(ld1_lds_v(q), ld1_lds_v(q + kMT), ld1_lds_v(q + 2 * kMT), ld1_lds_v(q + 3 * kMT));
+      if (LW == kLoadRowVecB) {
+        w = ld4_lds_v(ws + wa4[k & 3] + 64 * (k >> 2));
+      } else {
+        const float *q = ws + wa + 16 * k * kMT;
+        w = make_float4(ld1_lds_v(q), ld1_lds_v(q + kMT), ld1_lds_v(q + 2 * kMT), ld1_lds_v(q + 3 * kMT));
+      }
     };
     float4 pa, qa, pb, qb;  // set p: even blocks, set q: odd blocks
     rd(0, pa, qa);
 #pragma unroll
-    for (int blk = 0; blk < kKC / 16; blk += 2) {
+    for (int blk = 0; blk < KC / 16; blk += 2) {
       rd(blk + 1, pb, qb);
       __builtin_amdgcn_sched_barrier(0);
       if (blk == 0 && s == 0) mfma_block4_first(acc, pa, qa);
       else mfma_block4(acc, pa, qa);
       if (blk == 0 && more) dma_x(nx, s + 1);
-      if (blk + 2 < kKC / 16) rd(blk + 2, pa, qa);
+      if (blk + 2 < KC / 16) rd(blk + 2, pa, qa);
       __builtin_amdgcn_sched_barrier(0);
       mfma_block4(acc, pb, qb);
       if (blk == 0 && more) dma_w(nw, s + 1);
@@ -1628,10 +1649,13 @@ ArrayP dot_ggml(const DotOperand &lhs, const DotOperand &rhs, int64_t B, int64_t
     // multiple of the tile, every stage full, non-negative strides, and the
     // largest byte offset within a batch below 2^31.
     const bool full_stages = ((K / 16) % (kKC / 16)) == 0 && K >= kKC;
-    auto buf_ok = [&](int64_t sf, int64_t sk, int64_t sb, int64_t rows) {
-      if (rows % kMT || !full_stages || sf < 0 || sk < 0 || sb < 0 || lhs.sb2 < 0 || rhs.sb2 < 0) return false;
+    auto in_range = [&](int64_t sf, int64_t sk, int64_t sb, int64_t rows) {
+      if (rows % kMT || sf < 0 || sk < 0 || sb < 0 || lhs.sb2 < 0 || rhs.sb2 < 0) return false;
       const int64_t top = ((rows - 1) * sf + (K - 1) * sk + 4) * 4;
       return top < ((int64_t)1 << 31);
+    };
+    auto buf_ok = [&](int64_t sf, int64_t sk, int64_t sb, int64_t rows) {
+      return full_stages && in_range(sf, sk, sb, rows);
     };
     if (((lx == kLoadRowVec && ln % 4 == 0) || lx == kLoadColQuad) && buf_ok(ln, lk, lb, N) &&
         ((lw == kLoadRowVec && rm % 4 == 0) || lw == kLoadColQuad) && buf_ok(rm, rk, rb, M)) {
@@ -1669,8 +1693,18 @@ ArrayP dot_ggml(const DotOperand &lhs, const DotOperand &rhs, int64_t B, int64_t
     // loads both operands straight into LDS, one workgroup per tile, at any
     // stage count (the denoiser's K = 256 and 512 products: 6.11 -> 5.57 ms
     // against the persistent kernel).
+    // Both operands along k in stages of 64 (Q K^T with K = 64) go straight
+    // into LDS as well.
     const int64_t stages = (K / 16 + kKC / 16 - 1) / (kKC / 16);
-    const bool direct = lx == kLoadRowVecB && lw == kLoadColQuadB;
+    int dkc = 0;
+    if (lx == kLoadRowVecB && (lw == kLoadColQuadB || lw == kLoadRowVecB)) {
+      dkc = kKC;
+    } else if (lx == kLoadRowVec && lw == kLoadRowVec && K % 64 == 0 && K >= 64 && ln % 4 == 0 && rm % 4 == 0 &&
+               in_range(ln, lk, lb, N) && in_range(rm, rk, rb, M)) {
+      dkc = 64;
+      lx = lw = kLoadRowVecB;
+    }
+    const bool direct = dkc > 0;
     const bool persist = stages <= kPersistStages && !direct;
     const unsigned lds = ep.gelu ? kDotLdsGelu : kDotLds;
     const unsigned grid = (unsigned)std::min<int64_t>(tiles, device_props().multiProcessorCount);  // one per CU
@@ -1682,7 +1716,12 @@ ArrayP dot_ggml(const DotOperand &lhs, const DotOperand &rhs, int64_t B, int64_t
     launch([=](hipStream_t s) {
       (void)kl, (void)kr, (void)ek;
       if (direct) {
-        dot_mfma8d_k<kLoadRowVecB, kLoadColQuadB><<<grid1, 512, 0, s>>>(X, W, N, M, K, tiles_m, ep, Y);
+        if (lw == kLoadColQuadB)
+          dot_mfma8d_k<kLoadRowVecB, kLoadColQuadB, kKC><<<grid1, 512, 0, s>>>(X, W, N, M, K, tiles_m, ep, Y);
+        else if (dkc == kKC)
+          dot_mfma8d_k<kLoadRowVecB, kLoadRowVecB, kKC><<<grid1, 512, 0, s>>>(X, W, N, M, K, tiles_m, ep, Y);
+        else
+          dot_mfma8d_k<kLoadRowVecB, kLoadRowVecB, 64><<<grid1, 512, 0, s>>>(X, W, N, M, K, tiles_m, ep, Y);
         return;
       }
 #define DOT_CASE(a, c)                                                                    \

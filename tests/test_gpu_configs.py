@@ -148,6 +148,40 @@ def test_dot_direct_lds_loads(oracle, B, N, M, K):
             shlo_hip.set_flavor(0)
 
 
+
+def dot_nt_module(B, N, M, K):
+    """[B,N,K] x [B,M,K] -> [B,N,M], both operands contiguous along k (Q K^T)."""
+    from shlo_hip.configs import t
+    a, b, o = t((B, N, K)), t((B, M, K)), t((B, N, M))
+    dn = ("#stablehlo.dot<lhs_batching_dimensions = [0], rhs_batching_dimensions = [0], "
+          "lhs_contracting_dimensions = [2], rhs_contracting_dimensions = [2]>")
+    return (f"module {{\n  func.func public @main(%a0: {a}, %a1: {b}) -> ({o}) {{\n"
+            f'    %0 = "stablehlo.dot_general"(%a0, %a1) {{dot_dimension_numbers = {dn}}} : ({a}, {b}) -> {o}\n'
+            f"    func.return %0 : {o}\n  }}\n}}\n")
+
+
+@pytest.mark.parametrize("B,N,M,K", [(2, 128, 192, 64), (3, 192, 128, 192), (8, 256, 320, 64),
+                                     (2, 128, 128, 256), (1, 64, 64, 640)])
+def test_dot_direct_lds_loads_both_along_k(oracle, B, N, M, K):
+    """Both operands contiguous along k, rows multiples of 64: straight into
+    LDS in stages of 64 (K = 64, 192; the second with three stages) or of 128
+    (K = 256, 640), the rhs stored and read as the lhs.  Both flavours, eager
+    and compiled."""
+    import shlo_hip
+    lhs, st = oracle.fill_normal(41, 1.0, B * N * K)
+    rhs, _ = oracle.fill_normal(41, 1.0, B * M * K, state=st)
+    lhs, rhs = lhs.reshape(B, N, K), rhs.reshape(B, M, K)
+    for flavor in (0, 1):
+        want = oracle.dot_general_bnk(lhs, rhs, flavor)
+        shlo_hip.set_flavor(flavor)
+        try:
+            for compile in (True, False):
+                got = run(dot_nt_module(B, N, M, K), [lhs, rhs], compile=compile)[0]
+                assert same_bits(got, want), (flavor, compile)
+        finally:
+            shlo_hip.set_flavor(0)
+
+
 def causal_logits(oracle, rows, cols, sigma=4.0, seed=7):
     x, _ = oracle.fill_normal(seed, sigma, rows * cols)
     x = x.reshape(rows, cols)
