@@ -614,7 +614,10 @@ __global__ void __launch_bounds__(512) dot_mfma8_k(MfmaOperand X, MfmaOperand W,
 //   rhs along k (LW = kLoadRowVecB): [64 columns][KC / 4 k-quads], swizzled
 //     and read as the lhs.
 // KC = 128 k per stage, or 64 for contractions in multiples of 64 (Q K^T
-// with K = 64: rows of 16 chunks, 4 rows per instruction).
+// with K = 64: rows of 16 chunks, 4 rows per instruction).  WAVES = 8: a
+// 64 x 64 tile, 140 KB of LDS, one workgroup per CU.  WAVES = 4 (KC = 64): a
+// 32 x 64 tile (two quadrants, two waves each) in 60 KB, so two workgroups
+// share a CU and one's loads and epilogue overlap the other's products.
 // The two stage buffers are separate LDS variables and the stage loop is
 // unrolled by two, so the buffer being filled and the one being read are
 // different objects to the compiler.  Chains, epilogue and stores are
@@ -623,20 +626,28 @@ typedef __attribute__((address_space(3))) void lds_void;
 typedef const volatile __attribute__((address_space(3))) float lds_f32;
 __device__ __forceinline__ float ld1_lds_v(const float *p) { return *(lds_f32 *)(p); }
 
-template <int LX, int LW, int KC>
-__global__ void __launch_bounds__(512) dot_mfma8d_k(MfmaOperand X, MfmaOperand W, int64_t N, int64_t M, int64_t K,
-                                                    int tiles_m, Epilogue ep, float *__restrict__ Y) {
+template <int LX, int LW, int KC, int WAVES>
+__global__ void __launch_bounds__(WAVES * 64, 2) dot_mfma8d_k(MfmaOperand X, MfmaOperand W, int64_t N, int64_t M,
+                                                           int64_t K, int tiles_m, Epilogue ep,
+                                                           float *__restrict__ Y) {
   static_assert(LX == kLoadRowVecB && (LW == kLoadColQuadB || LW == kLoadRowVecB), "direct loads: lhs along k");
   static_assert(KC == 128 || KC == 64, "stages of 128 or 64 k");
-  constexpr int kChunks = kMT * kKC / 4;  // 16-byte chunks per buffer (a stage of KC = 64 uses half)
-  constexpr int CPR = KC / 4, RPI = 64 / CPR, NI = KC / 32;  // chunks per row, rows per instruction, instructions per wave
-  __shared__ float4 dx0[kChunks], dx1[kChunks], dw0[kChunks], dw1[kChunks];
+  static_assert(WAVES == 8 || (WAVES == 4 && KC == 64), "four waves with stages of 64");
+  constexpr int TN = WAVES == 8 ? kMT : 32;  // tile rows
+  // 16-byte chunks per buffer: the eight-wave kernel keeps 32 KB buffers (its
+  // epilogue exchange, 8 KB per wave, uses the lhs buffers); the four-wave one
+  // exchanges through the rhs buffers.
+  constexpr int XCH = WAVES == 8 ? kMT * kKC / 4 : TN * KC / 4, WCH = WAVES == 8 ? kMT * kKC / 4 : kMT * KC / 4;
+  constexpr int CPR = KC / 4, RPI = 64 / CPR;  // chunks per row, rows per instruction
+  constexpr int NIX = TN * KC / 4 / 64 / WAVES, NIW = kMT * KC / 4 / 64 / WAVES;  // instructions per wave
+  static_assert((RPI * WAVES) % 16 == 0, "the swizzle key of a row does not depend on the instruction");
+  __shared__ float4 dx0[XCH], dx1[XCH], dw0[WCH], dw1[WCH];
   __shared__ double gtab[kPolyWords];  // a fused gelu_erf's table
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int quad = wave & 3, rh = wave >> 2;
-  const int wn = quad >> 1, wm = quad & 1;
+  const int quad = wave % (WAVES / 2), rh = wave / (WAVES / 2);
+  const int wn = WAVES == 8 ? quad >> 1 : 0, wm = WAVES == 8 ? quad & 1 : quad;
   const int64_t b = blockIdx.y;
-  const int64_t n0 = (int64_t)(blockIdx.x / tiles_m) * kMT, m0 = (int64_t)(blockIdx.x % tiles_m) * kMT;
+  const int64_t n0 = (int64_t)(blockIdx.x / tiles_m) * TN, m0 = (int64_t)(blockIdx.x % tiles_m) * kMT;
   const int nst = (int)(K / KC);  // every stage full (the host checks)
 
   const int64_t nl = n0 + wn * 32 + 4 * (lane >> 5) + 16 * rh, ml = m0 + wm * 32 + (lane & 31);
@@ -664,16 +675,16 @@ __global__ void __launch_bounds__(512) dot_mfma8d_k(MfmaOperand X, MfmaOperand W
                         : (int)(((m0 + xr) * W.sf + 4 * ((lane % CPR) ^ (xr & 15))) * 4);
   auto dma_x = [&](float4 *dx, int s) {
 #pragma unroll
-    for (int i = 0; i < NI; i++)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(bx, (lds_void *)(dx + 64 * (8 * i + wv)), 16, xvoff,
-                                               (int)((8 * RPI * i * X.sf + (int64_t)KC * s) * 4), 0, 0);
+    for (int i = 0; i < NIX; i++)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(bx, (lds_void *)(dx + 64 * (WAVES * i + wv)), 16, xvoff,
+                                               (int)((WAVES * RPI * i * X.sf + (int64_t)KC * s) * 4), 0, 0);
   };
   auto dma_w = [&](float4 *dw, int s) {
 #pragma unroll
-    for (int i = 0; i < NI; i++) {
-      const int so = LW == kLoadColQuadB ? (int)(((int64_t)32 * i + (int64_t)KC * s) * W.sk * 4)
-                                         : (int)((8 * RPI * i * W.sf + (int64_t)KC * s) * 4);
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(bw, (lds_void *)(dw + 64 * (8 * i + wv)), 16, wvoff, so, 0, 0);
+    for (int i = 0; i < NIW; i++) {
+      const int so = LW == kLoadColQuadB ? (int)(((int64_t)4 * WAVES * i + (int64_t)KC * s) * W.sk * 4)
+                                         : (int)((WAVES * RPI * i * W.sf + (int64_t)KC * s) * 4);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(bw, (lds_void *)(dw + 64 * (WAVES * i + wv)), 16, wvoff, so, 0, 0);
     }
   };
 
@@ -733,14 +744,17 @@ __global__ void __launch_bounds__(512) dot_mfma8d_k(MfmaOperand X, MfmaOperand W
   }
 
   // Epilogue: dot_mfma8_k's, the exchange in the lhs buffers (waves 0..3 in
-  // dx0, 4..7 in dx1; no load is outstanding after the last stage).
+  // dx0, 4..7 in dx1; four waves: the rhs buffers; no load is outstanding
+  // after the last stage).
   float t4[16][4];
 #pragma unroll
   for (int r = 0; r < 16; r++)
 #pragma unroll
     for (int q = 0; q < 4; q++) t4[r][q] = acc[q][r] + acc[q][r + 16];
-  float *give = reinterpret_cast<float *>(rh ? dx1 : dx0) + quad * (8 * 4 * 64);  // [r % 8][q][lane]
-  const float *take = reinterpret_cast<const float *>(rh ? dx0 : dx1) + quad * (8 * 4 * 64);
+  static_assert((WAVES / 2) * 8 * 4 * 64 <= 4 * (WAVES == 8 ? XCH : WCH), "the exchange fits its buffers");
+  float *give = reinterpret_cast<float *>(WAVES == 8 ? (rh ? dx1 : dx0) : (rh ? dw1 : dw0)) + quad * (8 * 4 * 64);
+  const float *take =
+      reinterpret_cast<const float *>(WAVES == 8 ? (rh ? dx0 : dx1) : (rh ? dw0 : dw1)) + quad * (8 * 4 * 64);
 #pragma unroll
   for (int r = 0; r < 8; r++)
 #pragma unroll
@@ -1706,22 +1720,32 @@ ArrayP dot_ggml(const DotOperand &lhs, const DotOperand &rhs, int64_t B, int64_t
     }
     const bool direct = dkc > 0;
     const bool persist = stages <= kPersistStages && !direct;
+    // Short direct contractions: four-wave workgroups on 32 x 64 tiles, two per CU.
+    const bool small = direct && K <= 512;
+    const dim3 grid_s((unsigned)(tiles_n64 * 2 * tiles_m64), (unsigned)B);
     const unsigned lds = ep.gelu ? kDotLdsGelu : kDotLds;
     const unsigned grid = (unsigned)std::min<int64_t>(tiles, device_props().multiProcessorCount);  // one per CU
     TileWalk tw{tiles, (int)tiles_n64, tiles_m, (int)(grid / tiles_b), (int)((grid % tiles_b) / tiles_m64),
                 (int)(grid % tiles_m64)};
     const dim3 grid1((unsigned)tiles_b, (unsigned)B);
-    if (!persist && tiles_b > 0x7FFFFFFF) fail("dot_general: too many output tiles");
+    if (!persist && (small ? 2 * tiles_b : tiles_b) > 0x7FFFFFFF) fail("dot_general: too many output tiles");
     const int tl = tail;
     launch([=](hipStream_t s) {
       (void)kl, (void)kr, (void)ek;
+      if (direct && small) {
+        if (lw == kLoadColQuadB)
+          dot_mfma8d_k<kLoadRowVecB, kLoadColQuadB, 64, 4><<<grid_s, 256, 0, s>>>(X, W, N, M, K, tiles_m, ep, Y);
+        else
+          dot_mfma8d_k<kLoadRowVecB, kLoadRowVecB, 64, 4><<<grid_s, 256, 0, s>>>(X, W, N, M, K, tiles_m, ep, Y);
+        return;
+      }
       if (direct) {
         if (lw == kLoadColQuadB)
-          dot_mfma8d_k<kLoadRowVecB, kLoadColQuadB, kKC><<<grid1, 512, 0, s>>>(X, W, N, M, K, tiles_m, ep, Y);
+          dot_mfma8d_k<kLoadRowVecB, kLoadColQuadB, kKC, 8><<<grid1, 512, 0, s>>>(X, W, N, M, K, tiles_m, ep, Y);
         else if (dkc == kKC)
-          dot_mfma8d_k<kLoadRowVecB, kLoadRowVecB, kKC><<<grid1, 512, 0, s>>>(X, W, N, M, K, tiles_m, ep, Y);
+          dot_mfma8d_k<kLoadRowVecB, kLoadRowVecB, kKC, 8><<<grid1, 512, 0, s>>>(X, W, N, M, K, tiles_m, ep, Y);
         else
-          dot_mfma8d_k<kLoadRowVecB, kLoadRowVecB, 64><<<grid1, 512, 0, s>>>(X, W, N, M, K, tiles_m, ep, Y);
+          dot_mfma8d_k<kLoadRowVecB, kLoadRowVecB, 64, 8><<<grid1, 512, 0, s>>>(X, W, N, M, K, tiles_m, ep, Y);
         return;
       }
 #define DOT_CASE(a, c)                                                                    \
