@@ -425,7 +425,7 @@ __device__ __forceinline__ void dot_epi_early(const Epilogue &ep, int64_t b, int
 // element-wise ops (the first kEpiEarly with operands `pre` loaded by
 // dot_epi_early).  `whole` (wave-uniform) says every output is in range and
 // there is no tail.
-template <class RowF, class ColF>
+template <int NE = kEpiEarly, class RowF, class ColF>
 __device__ __forceinline__ void dot_store8(const MfmaOperand &X, const MfmaOperand &W, int64_t b, int64_t N,
                                            int64_t M, int64_t K, int64_t np, int tail, bool whole,
                                            const float (&out)[8], const Epilogue &ep, const float (&pre)[kEpiEarly][8],
@@ -460,9 +460,9 @@ __device__ __forceinline__ void dot_store8(const MfmaOperand &X, const MfmaOpera
   }
   if (ep.n > 0) {
     auto gelu = [&](float x) { return gelu1<0>(x, gtab); };
-    epi_ops_n(ep, v, pre, gelu);
+    if (NE > 0) epi_ops_n(ep, v, pre, gelu);
     epi_apply_n(
-        ep, v, [&](const EpiOp &o, int r) { return dot_epi_off(o, b, N, M, r, row, col); }, kEpiEarly, gelu);
+        ep, v, [&](const EpiOp &o, int r) { return dot_epi_off(o, b, N, M, r, row, col); }, NE, gelu);
   }
   float *y = Y + b * N * M;
   if (whole) {
@@ -642,7 +642,11 @@ __global__ void __launch_bounds__(WAVES * 64, 2) dot_mfma8d_k(MfmaOperand X, Mfm
   constexpr int NIX = TN * KC / 4 / 64 / WAVES, NIW = kMT * KC / 4 / 64 / WAVES;  // instructions per wave
   static_assert((RPI * WAVES) % 16 == 0, "the swizzle key of a row does not depend on the instruction");
   __shared__ float4 dx0[XCH], dx1[XCH], dw0[WCH], dw1[WCH];
-  __shared__ double gtab[kPolyWords];  // a fused gelu_erf's table
+  extern __shared__ double gtab[];  // a fused gelu_erf's table (dynamic LDS, only with one)
+  // The eight-wave kernel loads the first fused ops' operands before the
+  // products; the four-wave one at the end (two more workgroups hide it, and
+  // 16 fewer registers let three share a CU).
+  constexpr int NE = WAVES == 8 ? kEpiEarly : 0;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int quad = wave % (WAVES / 2), rh = wave / (WAVES / 2);
   const int wn = WAVES == 8 ? quad >> 1 : 0, wm = WAVES == 8 ? quad & 1 : quad;
@@ -654,7 +658,7 @@ __global__ void __launch_bounds__(WAVES * 64, 2) dot_mfma8d_k(MfmaOperand X, Mfm
   auto orow = [&](int r) { return nl + 8 * (r / 4) + r % 4; };
   auto ocol = [&](int) { return ml; };
   float pre[kEpiEarly][8];
-  dot_epi_early(ep, b, N, M, pre, orow, ocol);
+  if (NE > 0) dot_epi_early(ep, b, N, M, pre, orow, ocol);
   if (ep.gelu) load_poly(gtab);
 
   // Loads.  Instruction i (0..NI-1) of wave w fills chunks 64 (8 i + w) .. + 63
@@ -771,7 +775,7 @@ __global__ void __launch_bounds__(WAVES * 64, 2) dot_mfma8d_k(MfmaOperand X, Mfm
     }
     out[r] = (w[0] + w[1]) + (w[2] + w[3]);  // vaddvq_f32
   }
-  dot_store8(X, W, b, N, M, K, K, kTailStock, true, out, ep, pre, gtab, Y, orow, ocol);
+  dot_store8<NE>(X, W, b, N, M, K, K, kTailStock, true, out, ep, pre, gtab, Y, orow, ocol);
 }
 
 
@@ -1722,6 +1726,7 @@ ArrayP dot_ggml(const DotOperand &lhs, const DotOperand &rhs, int64_t B, int64_t
     const bool persist = stages <= kPersistStages && !direct;
     // Short direct contractions: four-wave workgroups on 32 x 64 tiles, two per CU.
     const bool small = direct && K <= 512;
+    const unsigned glds = ep.gelu ? kPolyWords * (unsigned)sizeof(double) : 0;  // the direct kernels' dynamic LDS
     const dim3 grid_s((unsigned)(tiles_n64 * 2 * tiles_m64), (unsigned)B);
     const unsigned lds = ep.gelu ? kDotLdsGelu : kDotLds;
     const unsigned grid = (unsigned)std::min<int64_t>(tiles, device_props().multiProcessorCount);  // one per CU
@@ -1734,18 +1739,18 @@ ArrayP dot_ggml(const DotOperand &lhs, const DotOperand &rhs, int64_t B, int64_t
       (void)kl, (void)kr, (void)ek;
       if (direct && small) {
         if (lw == kLoadColQuadB)
-          dot_mfma8d_k<kLoadRowVecB, kLoadColQuadB, 64, 4><<<grid_s, 256, 0, s>>>(X, W, N, M, K, tiles_m, ep, Y);
+          dot_mfma8d_k<kLoadRowVecB, kLoadColQuadB, 64, 4><<<grid_s, 256, glds, s>>>(X, W, N, M, K, tiles_m, ep, Y);
         else
-          dot_mfma8d_k<kLoadRowVecB, kLoadRowVecB, 64, 4><<<grid_s, 256, 0, s>>>(X, W, N, M, K, tiles_m, ep, Y);
+          dot_mfma8d_k<kLoadRowVecB, kLoadRowVecB, 64, 4><<<grid_s, 256, glds, s>>>(X, W, N, M, K, tiles_m, ep, Y);
         return;
       }
       if (direct) {
         if (lw == kLoadColQuadB)
-          dot_mfma8d_k<kLoadRowVecB, kLoadColQuadB, kKC, 8><<<grid1, 512, 0, s>>>(X, W, N, M, K, tiles_m, ep, Y);
+          dot_mfma8d_k<kLoadRowVecB, kLoadColQuadB, kKC, 8><<<grid1, 512, glds, s>>>(X, W, N, M, K, tiles_m, ep, Y);
         else if (dkc == kKC)
-          dot_mfma8d_k<kLoadRowVecB, kLoadRowVecB, kKC, 8><<<grid1, 512, 0, s>>>(X, W, N, M, K, tiles_m, ep, Y);
+          dot_mfma8d_k<kLoadRowVecB, kLoadRowVecB, kKC, 8><<<grid1, 512, glds, s>>>(X, W, N, M, K, tiles_m, ep, Y);
         else
-          dot_mfma8d_k<kLoadRowVecB, kLoadRowVecB, 64, 8><<<grid1, 512, 0, s>>>(X, W, N, M, K, tiles_m, ep, Y);
+          dot_mfma8d_k<kLoadRowVecB, kLoadRowVecB, 64, 8><<<grid1, 512, glds, s>>>(X, W, N, M, K, tiles_m, ep, Y);
         return;
       }
 #define DOT_CASE(a, c)                                                                    \
