@@ -60,6 +60,12 @@ struct NoUnary {
   __device__ float operator()(float v) const { return v; }
 };
 
+// Whether an op's operand takes one value over the NV values a lane holds
+// (then one load serves them all); by default never.
+struct NeverUniform {
+  __device__ bool operator()(const EpiOp &) const { return false; }
+};
+
 template <class Unary = NoUnary>
 __device__ __forceinline__ float epi_apply(const Epilogue &e, float v, int64_t i0, int64_t i1, int64_t i2,
                                            Unary un = Unary()) {
@@ -91,12 +97,18 @@ __device__ __forceinline__ void epi_op(float (&v)[NV], const float (&w)[NV], uin
 // The same in two steps, for a producer that can issue the operand loads
 // long before its values are ready: epi_load_n, then epi_ops_n, for the first
 // NE ops (epi_apply_n's `from` then takes the rest).
-template <int NE, int NV, class Off>
-__device__ __forceinline__ void epi_load_n(const Epilogue &e, float (&w)[NE][NV], Off off) {
+template <int NE, int NV, class Off, class Uni = NeverUniform>
+__device__ __forceinline__ void epi_load_n(const Epilogue &e, float (&w)[NE][NV], Off off, Uni uni = Uni()) {
 #pragma unroll
   for (int k = 0; k < NE; k++) {
     if (k >= e.n) break;
     if (e.op[k].code == kEpiGeluErf) continue;
+    if (uni(e.op[k])) {
+      const float w0 = e.op[k].p[off(e.op[k], 0)];
+#pragma unroll
+      for (int r = 0; r < NV; r++) w[k][r] = w0;
+      continue;
+    }
 #pragma unroll
     for (int r = 0; r < NV; r++) w[k][r] = e.op[k].p[off(e.op[k], r)];
   }
@@ -126,9 +138,9 @@ __device__ __forceinline__ void epi_ops_n(const Epilogue &e, float (&v)[NV], con
   }
 }
 
-template <int NV, class Off, class Unary = NoUnary>
+template <int NV, class Off, class Unary = NoUnary, class Uni = NeverUniform>
 __device__ __forceinline__ void epi_apply_n(const Epilogue &e, float (&v)[NV], Off off, int from = 0,
-                                            Unary un = Unary()) {
+                                            Unary un = Unary(), Uni uni = Uni()) {
 #pragma unroll
   for (int k = 0; k < kMaxEpi; k++) {
     if (k < from) continue;
@@ -140,8 +152,14 @@ __device__ __forceinline__ void epi_apply_n(const Epilogue &e, float (&v)[NV], O
       continue;
     }
     float w[NV];
+    if (uni(o)) {
+      const float w0 = o.p[off(o, 0)];
 #pragma unroll
-    for (int r = 0; r < NV; r++) w[r] = o.p[off(o, r)];
+      for (int r = 0; r < NV; r++) w[r] = w0;
+    } else {
+#pragma unroll
+      for (int r = 0; r < NV; r++) w[r] = o.p[off(o, r)];
+    }
     switch (o.code) {
       case kAdd: epi_op<kAdd>(v, w, o.rev); break;
       case kSub: epi_op<kSub>(v, w, o.rev); break;

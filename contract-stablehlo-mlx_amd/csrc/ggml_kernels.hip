@@ -414,10 +414,20 @@ __device__ __forceinline__ int64_t dot_epi_off(const EpiOp &o, int64_t b, int64_
   return b * o.s0 + (nr < N ? nr : N - 1) * o.s1 + (mr < M ? mr : M - 1) * o.s2;
 }
 
-template <class RowF, class ColF>
+// Whether a fused op's operand is one value over a lane's 8 outputs: the
+// 32x32-layout kernels' 8 outputs share a column (COLCONST), so an operand
+// broadcast along rows (a bias) or a scalar is; in the 16x16 layout only a
+// scalar per batch is.
+template <bool COLCONST>
+struct DotUniform {
+  __device__ bool operator()(const EpiOp &o) const { return o.s1 == 0 && (COLCONST || o.s2 == 0); }
+};
+
+template <bool COLCONST, class RowF, class ColF>
 __device__ __forceinline__ void dot_epi_early(const Epilogue &ep, int64_t b, int64_t N, int64_t M,
                                               float (&pre)[kEpiEarly][8], RowF row, ColF col) {
-  epi_load_n(ep, pre, [&](const EpiOp &o, int r) { return dot_epi_off(o, b, N, M, r, row, col); });
+  epi_load_n(
+      ep, pre, [&](const EpiOp &o, int r) { return dot_epi_off(o, b, N, M, r, row, col); }, DotUniform<COLCONST>());
 }
 
 // Stores the 8 outputs a lane finishes, output r at row row(r) and column
@@ -425,7 +435,7 @@ __device__ __forceinline__ void dot_epi_early(const Epilogue &ep, int64_t b, int
 // element-wise ops (the first kEpiEarly with operands `pre` loaded by
 // dot_epi_early).  `whole` (wave-uniform) says every output is in range and
 // there is no tail.
-template <int NE = kEpiEarly, class RowF, class ColF>
+template <bool COLCONST, int NE = kEpiEarly, class RowF, class ColF>
 __device__ __forceinline__ void dot_store8(const MfmaOperand &X, const MfmaOperand &W, int64_t b, int64_t N,
                                            int64_t M, int64_t K, int64_t np, int tail, bool whole,
                                            const float (&out)[8], const Epilogue &ep, const float (&pre)[kEpiEarly][8],
@@ -462,7 +472,8 @@ __device__ __forceinline__ void dot_store8(const MfmaOperand &X, const MfmaOpera
     auto gelu = [&](float x) { return gelu1<0>(x, gtab); };
     if (NE > 0) epi_ops_n(ep, v, pre, gelu);
     epi_apply_n(
-        ep, v, [&](const EpiOp &o, int r) { return dot_epi_off(o, b, N, M, r, row, col); }, NE, gelu);
+        ep, v, [&](const EpiOp &o, int r) { return dot_epi_off(o, b, N, M, r, row, col); }, NE, gelu,
+        DotUniform<COLCONST>());
   }
   float *y = Y + b * N * M;
   if (whole) {
@@ -504,7 +515,7 @@ __global__ void __launch_bounds__(512) dot_mfma8_k(MfmaOperand X, MfmaOperand W,
   auto orow = [&](int r) { return nl + 8 * (r / 4) + r % 4; };
   auto ocol = [&](int) { return ml; };
   float pre[kEpiEarly][8];
-  dot_epi_early(ep, b, N, M, pre, orow, ocol);
+  dot_epi_early<true>(ep, b, N, M, pre, orow, ocol);
   double *gtab = reinterpret_cast<double *>(lds_m + kDotStageFloats);  // a fused gelu_erf's table
   if (ep.gelu) load_poly(gtab);
 
@@ -592,7 +603,7 @@ __global__ void __launch_bounds__(512) dot_mfma8_k(MfmaOperand X, MfmaOperand W,
     }
     out[r] = (w[0] + w[1]) + (w[2] + w[3]);  // vaddvq_f32
   }
-  dot_store8(X, W, b, N, M, K, np, tail, np == K && n0 + kMT <= N && m0 + kMT <= M, out, ep, pre, gtab, Y, orow,
+  dot_store8<true>(X, W, b, N, M, K, np, tail, np == K && n0 + kMT <= N && m0 + kMT <= M, out, ep, pre, gtab, Y, orow,
              ocol);
 }
 
@@ -658,7 +669,7 @@ __global__ void __launch_bounds__(WAVES * 64, 2) dot_mfma8d_k(MfmaOperand X, Mfm
   auto orow = [&](int r) { return nl + 8 * (r / 4) + r % 4; };
   auto ocol = [&](int) { return ml; };
   float pre[kEpiEarly][8];
-  if (NE > 0) dot_epi_early(ep, b, N, M, pre, orow, ocol);
+  if (NE > 0) dot_epi_early<true>(ep, b, N, M, pre, orow, ocol);
   if (ep.gelu) load_poly(gtab);
 
   // Loads.  Instruction i (0..NI-1) of wave w fills chunks 64 (8 i + w) .. + 63
@@ -775,7 +786,7 @@ __global__ void __launch_bounds__(WAVES * 64, 2) dot_mfma8d_k(MfmaOperand X, Mfm
     }
     out[r] = (w[0] + w[1]) + (w[2] + w[3]);  // vaddvq_f32
   }
-  dot_store8<NE>(X, W, b, N, M, K, K, kTailStock, true, out, ep, pre, gtab, Y, orow, ocol);
+  dot_store8<true, NE>(X, W, b, N, M, K, K, kTailStock, true, out, ep, pre, gtab, Y, orow, ocol);
 }
 
 
@@ -879,7 +890,7 @@ __global__ void __launch_bounds__(512) dot_mfma16p_k(MfmaOperand X, MfmaOperand 
     auto orow = [&](int r) { return nbase + r % 4; };
     auto ocol = [&](int r) { return mbase + 16 * (r / 4); };
     float pre[kEpiEarly][8];
-    dot_epi_early(ep, b, N, M, pre, orow, ocol);
+    dot_epi_early<false>(ep, b, N, M, pre, orow, ocol);
     for (int s = 0; s < nst; s++) {
       const float *xs = tile(buf, 0) + (wr * 16 + l16) * kLS + 4 * kq;
       const float *ws = tile(buf, 1) + (wc * 32 + l16) * kLS + 4 * kq;
@@ -941,7 +952,7 @@ __global__ void __launch_bounds__(512) dot_mfma16p_k(MfmaOperand X, MfmaOperand 
           s4[g] = (acc[c][g][ii] + acc[c][g][8 + ii]) + (acc[c][g][4 + ii] + acc[c][g][12 + ii]);
         out[4 * c + ii] = (s4[0] + s4[1]) + (s4[2] + s4[3]);
       }
-    dot_store8(X, W, b, N, M, K, np, tail, np == K && n0 + kMT <= N && m0 + kMT <= M, out, ep, pre, gtab, Y,
+    dot_store8<false>(X, W, b, N, M, K, np, tail, np == K && n0 + kMT <= N && m0 + kMT <= M, out, ep, pre, gtab, Y,
                orow, ocol);
     if (!has_next) break;
     t = tn;
