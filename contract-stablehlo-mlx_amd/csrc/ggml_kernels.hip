@@ -1394,11 +1394,31 @@ __global__ void __launch_bounds__(256) norm_rows_k(int64_t rows, int cols, float
   // out now and land under the reductions.
   float w[kEpiEarly][4 * J], wt[kEpiEarly][1];  // the first kEpiEarly ops' operands; later ops load at the end
   if (EPI) {
-    epi_load_n(ep, w, [&](const EpiOp &o, int r) {
-      const int g = lane + kWave * (r / 4);
-      const int c = (FULL || g < G) ? 4 * g + r % 4 : 0;  // a discarded group reads column 0
-      return row * o.s1 + c * o.s2;
-    });
+    // An operand along columns with unit stride from a 16-byte aligned start
+    // (LayerNorm's gain and bias) loads float4 groups, as the row does;
+    // any other, one element at a time.
+#pragma unroll
+    for (int k = 0; k < kEpiEarly; k++) {
+      if (k >= ep.n) break;
+      const EpiOp &o = ep.op[k];
+      if (o.code == kEpiGeluErf) continue;
+      const float *base = o.p + row * o.s1;
+      if (o.s2 == 1 && T == 0 && ((uintptr_t)base & 15) == 0) {
+#pragma unroll
+        for (int j = 0; j < J; j++) {
+          const int g = lane + kWave * j;
+          const float4 q = ld4(base + 4 * ((FULL || g < G) ? g : 0));  // a discarded group reads group 0
+          w[k][4 * j] = q.x, w[k][4 * j + 1] = q.y, w[k][4 * j + 2] = q.z, w[k][4 * j + 3] = q.w;
+        }
+      } else {
+#pragma unroll
+        for (int r = 0; r < 4 * J; r++) {
+          const int g = lane + kWave * (r / 4);
+          const int c = (FULL || g < G) ? 4 * g + r % 4 : 0;  // a discarded group reads column 0
+          w[k][r] = o.p[row * o.s1 + c * o.s2];
+        }
+      }
+    }
     if (T > 0) epi_load_n(ep, wt, [&](const EpiOp &o, int) { return row * o.s1 + (lane < T ? 4 * G + lane : 0) * o.s2; });
   }
   double ls = 0.0, la = 0.0;

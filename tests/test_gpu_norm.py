@@ -166,6 +166,36 @@ def test_fused_affine(oracle, shape):
     check(oracle, x, ((g + F32(1)).astype(F32), b))
 
 
+@pytest.mark.parametrize("kind", ["slice", "transpose"])
+def test_fused_operand_layouts(oracle, kind):
+    """norm(x) * y + b where y is a view the fused loads cannot take as
+    16-byte groups: a slice starting one element into each row (misaligned)
+    or a transposed array (column stride 64); b is an aligned bias."""
+    R, C = 64, 512
+    x, st = oracle.fill_normal(71, 1.0, R * C)
+    x = x.reshape(R, C)
+    zsh = (R, C + 4) if kind == "slice" else (C, R)
+    z, st = oracle.fill_normal(72, 1.0, zsh[0] * zsh[1], state=st)
+    z = z.reshape(zsh)
+    b, _ = oracle.fill_normal(73, 0.5, C, state=st)
+    y = z[:, 1:C + 1] if kind == "slice" else z.T
+    want = ((oracle.norm(x) * y).astype(F32) + b).astype(F32)
+    s, zt = t((R, C)), t(zsh)
+    if kind == "slice":
+        view = (f'    %y = "stablehlo.slice"(%z) {{start_indices = array<i64: 0, 1>, limit_indices = '
+                f'array<i64: {R}, {C + 1}>, strides = array<i64: 1, 1>}} : ({zt}) -> {s}\n')
+    else:
+        view = f'    %y = "stablehlo.transpose"(%z) {{permutation = array<i64: 1, 0>}} : ({zt}) -> {s}\n'
+    text = (f"module {{\n  func.func public @main(%x: {s}, %z: {zt}, %b: {t((C,))}) -> ({s}) {{\n" + view +
+            f'    %0 = "stablehlo.custom_call"(%x) {{call_target_name = "ggml.norm", backend_config = "{EPS}"}} : ({s}) -> {s}\n'
+            f'    %1 = "stablehlo.multiply"(%0, %y) : ({s}, {s}) -> {s}\n'
+            f'    %bb = "stablehlo.broadcast_in_dim"(%b) {{broadcast_dimensions = array<i64: 1>}} : ({t((C,))}) -> {s}\n'
+            f'    %2 = "stablehlo.add"(%1, %bb) : ({s}, {s}) -> {s}\n'
+            f"    func.return %2 : {s}\n  }}\n}}\n")
+    for compile in (True, False):
+        assert same_bits(run(text, [x, z, b], compile=compile), want), compile
+
+
 def test_planted_norm_fault_differs(oracle):
     import shlo_hip
     x, _ = oracle.fill_normal(30, 1.0, 64 * 512)
