@@ -671,7 +671,10 @@ __global__ void __launch_bounds__(WAVES * 64, 2) dot_mfma8d_k(MfmaOperand X, Mfm
   auto ocol = [&](int) { return ml; };
   float pre[kEpiEarly][8];
   if (NE > 0) dot_epi_early<true>(ep, b, N, M, pre, orow, ocol);
-  if (ep.gelu) load_poly(gtab);
+  // The four-wave form reads a fused GELU's table from global memory (cached),
+  // keeping its LDS at 48 KB so that three workgroups share a CU.
+  const double *gt = WAVES == 4 ? &erffk::kPoly[0][0] : gtab;
+  if (WAVES == 8 && ep.gelu) load_poly(gtab);
 
   // Loads.  Instruction i (0..NI-1) of wave w fills chunks 64 (8 i + w) .. + 63
   // of each operand: lhs rows RPI (8 i + w) + lane / CPR (lane % CPR is the
@@ -789,7 +792,7 @@ __global__ void __launch_bounds__(WAVES * 64, 2) dot_mfma8d_k(MfmaOperand X, Mfm
     }
     out[r] = (w[0] + w[1]) + (w[2] + w[3]);  // vaddvq_f32
   }
-  dot_store8<true, NE>(X, W, b, N, M, K, K, kTailStock, true, out, ep, pre, gtab, Y, orow, ocol);
+  dot_store8<true, NE>(X, W, b, N, M, K, K, kTailStock, true, out, ep, pre, gt, Y, orow, ocol);
 }
 
 
@@ -1760,7 +1763,7 @@ ArrayP dot_ggml(const DotOperand &lhs, const DotOperand &rhs, int64_t B, int64_t
     const bool persist = stages <= kPersistStages && !direct;
     // Short direct contractions: four-wave workgroups on 32 x 64 tiles, two per CU.
     const bool small = direct && K <= 512;
-    const unsigned glds = ep.gelu ? kPolyWords * (unsigned)sizeof(double) : 0;  // the direct kernels' dynamic LDS
+    const unsigned glds = ep.gelu ? kPolyWords * (unsigned)sizeof(double) : 0;  // the eight-wave direct kernel's dynamic LDS
     const dim3 grid_s((unsigned)(tiles_n64 * 2 * tiles_m64), (unsigned)B);
     const unsigned lds = ep.gelu ? kDotLdsGelu : kDotLds;
     const unsigned grid = (unsigned)std::min<int64_t>(tiles, device_props().multiProcessorCount);  // one per CU
@@ -1773,9 +1776,9 @@ ArrayP dot_ggml(const DotOperand &lhs, const DotOperand &rhs, int64_t B, int64_t
       (void)kl, (void)kr, (void)ek;
       if (direct && small) {
         if (lw == kLoadColQuadB)
-          dot_mfma8d_k<kLoadRowVecB, kLoadColQuadB, 64, 4><<<grid_s, 256, glds, s>>>(X, W, N, M, K, tiles_m, ep, Y);
+          dot_mfma8d_k<kLoadRowVecB, kLoadColQuadB, 64, 4><<<grid_s, 256, 0, s>>>(X, W, N, M, K, tiles_m, ep, Y);
         else
-          dot_mfma8d_k<kLoadRowVecB, kLoadRowVecB, 64, 4><<<grid_s, 256, glds, s>>>(X, W, N, M, K, tiles_m, ep, Y);
+          dot_mfma8d_k<kLoadRowVecB, kLoadRowVecB, 64, 4><<<grid_s, 256, 0, s>>>(X, W, N, M, K, tiles_m, ep, Y);
         return;
       }
       if (direct) {
