@@ -796,187 +796,10 @@ __global__ void __launch_bounds__(WAVES * 64, 2) dot_mfma8d_k(MfmaOperand X, Mfm
 }
 
 
-// The persistent kernel's tile walk: tiles (b, nt, mt) in row-major order over
-// (B, tiles_n, tiles_m), and gridDim.x = (db * tiles_n + dnt) * tiles_m + dmt
-// with dnt < tiles_n, dmt < tiles_m.
-struct TileWalk {
-  int64_t tiles;
-  int tiles_n, tiles_m, db, dnt, dmt;
-};
-
-// ---- the 16x16 layout: every chain of an output in one lane -------------------------
-//
-// v_mfma_f32_16x16x1_4b_f32 adds one product to each output of four 16x16
-// blocks: lane l supplies A of block l/16 row l%16 and B of block l/16
-// column l%16, and block b's output (i, j) sits in lane j + 16 (i/4),
-// register 4b + i%4 (checked bit for bit against fmaf, as the 32x32 one).
-// A lane reads one float4 along k (k 16 blk + 4 (l/16) ..), so in the four
-// instructions g = 0..3 of a block, block b carries residue 4b + g: the 16
-// chains of an output (i, j) are the 16 (b, g) values of one lane, and the
-// ggml tree runs in registers with no exchange between waves.  A wave owns
-// 16 rows x 32 columns (two column blocks, 8 accumulator sets, 128 registers);
-// per block it reads one float4 of the lhs and two of the rhs and issues 8
-// instructions.  The LDS layout, the loaders and the stage schedule are
-// dot_mfma8_k's; the epilogue needs neither LDS nor a barrier.
-//
-// Persistent form: one workgroup per CU walks output tiles t = blockIdx.x,
-// blockIdx.x + gridDim.x, ..., and its stage pipeline runs straight across
-// tile boundaries, so the next tile's loads and LDS writes overlap this
-// tile's last stage and epilogue (a tile with K = 64 has one short stage).
-// Tiles run round-robin, so the workgroups that share an rhs tile at one time
-// sit on one XCD (for 4 row tiles per rhs tile).
-// Against the 32x32 layout in the same persistent form (the chains split
-// between two waves, one value per output exchanged through LDS between two
-// more barriers) attention went from 0.128 to 0.123 ms and the denoiser from
-// 6.50 to 6.39 ms.  Long contractions keep one workgroup per tile
-// (dot_mfma8_k): config 3 ran 5.44 ms persistent in this layout, 5.37
-// persistent in the 32x32 one, 5.16 per tile.
-typedef float v16f __attribute__((ext_vector_type(16)));
-
-__device__ __forceinline__ void mfma16_block(v16f (&acc)[2][4], const float4 &x, const float4 &w0, const float4 &w1,
-                                             bool first) {
-  const v16f z = {};
-  const float xv[4] = {x.x, x.y, x.z, x.w}, w0v[4] = {w0.x, w0.y, w0.z, w0.w}, w1v[4] = {w1.x, w1.y, w1.z, w1.w};
-#pragma unroll
-  for (int g = 0; g < 4; g++) {
-    acc[0][g] = __builtin_amdgcn_mfma_f32_16x16x1f32(xv[g], w0v[g], first ? z : acc[0][g], 0, 0, 0);
-    acc[1][g] = __builtin_amdgcn_mfma_f32_16x16x1f32(xv[g], w1v[g], first ? z : acc[1][g], 0, 0, 0);
-  }
-}
-
-template <int LX, int LW>
-__global__ void __launch_bounds__(512) dot_mfma16p_k(MfmaOperand X, MfmaOperand W, int64_t N, int64_t M, int64_t K,
-                                                     int tail, TileWalk tw, Epilogue ep, float *__restrict__ Y) {
-  constexpr int TH = 512, R = regs_of<TH>();
-  extern __shared__ float lds_m[];  // [buffer][operand][kMT * kLS]
-  auto tile = [&](int buf, int op) { return lds_m + (buf * 2 + op) * (kMT * kLS); };
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int wr = wave >> 1, wc = wave & 1;  // rows 16 wr .., columns 32 wc ..
-  const int l16 = lane & 15, kq = lane >> 4;
-  const int64_t np = K & ~(int64_t)15;
-  const int nb = (int)(np / 16);
-  const int nst = (nb + kKC / 16 - 1) / (kKC / 16);
-  int64_t t = blockIdx.x;  // the host launches at most `tiles` workgroups
-  const int tiles_b = tw.tiles_n * tw.tiles_m;
-  int b = (int)blockIdx.x / tiles_b, nt = ((int)blockIdx.x % tiles_b) / tw.tiles_m, mt = (int)blockIdx.x % tw.tiles_m;
-  int64_t n0 = (int64_t)nt * kMT, m0 = (int64_t)mt * kMT;
-  BufOp bx = buf_op<LX>(X, b, n0), bw = buf_op<LW>(W, b, m0);
-  double *gtab = reinterpret_cast<double *>(lds_m + kDotStageFloats);  // a fused gelu_erf's table
-  if (ep.gelu) load_poly(gtab);
-
-  float4 rx[R], rw[R];
-  if (nst > 0) {
-    mfma_fetch<LX, TH>(X, bx, n0, 0, nb, rx);
-    mfma_fetch<LW, TH>(W, bw, m0, 0, nb, rw);
-    mfma_stash<LX, TH>(tile(0, 0), rx);
-    mfma_stash<LW, TH>(tile(0, 1), rw);
-  }
-  __syncthreads();
-  int buf = 0;
-  v16f acc[2][4];
-  for (;;) {
-    if (nst == 0) {  // K < 16: no block; the tail starts from the +0 tree
-#pragma unroll
-      for (int c = 0; c < 2; c++)
-#pragma unroll
-        for (int g = 0; g < 4; g++)
-#pragma unroll
-          for (int r = 0; r < 16; r++) acc[c][g][r] = 0.0f;
-    }
-    const int64_t tn = t + gridDim.x;
-    const bool has_next = tn < tw.tiles;
-    int mt_ = mt + tw.dmt, nt_ = nt + tw.dnt, b_ = b + tw.db;
-    if (mt_ >= tw.tiles_m) mt_ -= tw.tiles_m, nt_++;
-    if (nt_ >= tw.tiles_n) nt_ -= tw.tiles_n, b_++;
-    const int nb_ = has_next ? b_ : b;
-    const int64_t nn0 = has_next ? (int64_t)nt_ * kMT : n0, nm0 = has_next ? (int64_t)mt_ * kMT : m0;
-    const BufOp nbx = buf_op<LX>(X, nb_, nn0), nbw = buf_op<LW>(W, nb_, nm0);
-    // This lane's 8 outputs: rows nbase + r % 4 of columns mbase + 16 (r / 4).
-    const int64_t nbase = n0 + wr * 16 + 4 * kq, mbase = m0 + wc * 32 + l16;
-    auto orow = [&](int r) { return nbase + r % 4; };
-    auto ocol = [&](int r) { return mbase + 16 * (r / 4); };
-    float pre[kEpiEarly][8];
-    dot_epi_early<false>(ep, b, N, M, pre, orow, ocol);
-    for (int s = 0; s < nst; s++) {
-      const float *xs = tile(buf, 0) + (wr * 16 + l16) * kLS + 4 * kq;
-      const float *ws = tile(buf, 1) + (wc * 32 + l16) * kLS + 4 * kq;
-      const int blocks = min(kKC / 16, nb - s * (kKC / 16));
-      const bool here = s + 1 < nst;
-      const bool more = here || has_next;
-      const int fs = here ? s + 1 : 0;
-      const int64_t fn0 = here ? n0 : nn0, fm0 = here ? m0 : nm0;
-      const BufOp &fbx = here ? bx : nbx;
-      const BufOp &fbw = here ? bw : nbw;
-      // dot_mfma8_k's schedule: straight-line blocks, block blk + 1's operands
-      // read (volatile, ahead of a scheduling barrier) before block blk's
-      // instructions issue; the next stage's loads after blocks 0 and 1, its
-      // LDS writes after blocks 4 and 5.
-      auto rd = [&](int k, float4 &x, float4 &w0, float4 &w1) {
-        const int o = 16 * (k < blocks ? k : blocks - 1);  // blocks >= 1 in every stage
-        x = ld4_lds_v(xs + o);
-        w0 = ld4_lds_v(ws + o);
-        w1 = ld4_lds_v(ws + 16 * kLS + o);
-      };
-      auto part = [&](int q) {
-        if (more) {
-          if (q == 0) mfma_fetch<LX, TH>(X, fbx, fn0, fs, nb, rx);
-          if (q == 1) mfma_fetch<LW, TH>(W, fbw, fm0, fs, nb, rw);
-          if (q == 4) mfma_stash<LX, TH>(tile(buf ^ 1, 0), rx);
-          if (q == 5) mfma_stash<LW, TH>(tile(buf ^ 1, 1), rw);
-        }
-        __builtin_amdgcn_sched_barrier(0);
-      };
-      float4 pa, pa0, pa1, pb, pb0, pb1;  // set p: even blocks, set q: odd blocks
-      rd(0, pa, pa0, pa1);
-#pragma unroll
-      for (int blk = 0; blk < kKC / 16; blk += 2) {
-        rd(blk + 1, pb, pb0, pb1);
-        __builtin_amdgcn_sched_barrier(0);
-        if (blk == 0 && s == 0) mfma16_block(acc, pa, pa0, pa1, true);
-        else if (blk < blocks) mfma16_block(acc, pa, pa0, pa1, false);
-        if (blk == 0 || blk == 4) part(blk);
-        if (blk + 2 < kKC / 16) rd(blk + 2, pa, pa0, pa1);
-        __builtin_amdgcn_sched_barrier(0);
-        if (blk + 1 < blocks) mfma16_block(acc, pb, pb0, pb1, false);
-        if (blk == 0 || blk == 4) part(blk + 1);
-      }
-      __syncthreads();
-      buf ^= 1;
-    }
-
-    // Epilogue: output (row 4 kq + ii, column 16 c + l16) of the wave's region
-    // holds residue 4b + g in register 4b + ii of set [c][g]: GGML_F32x4_REDUCE
-    // lane g is (a[g] + a[8+g]) + (a[4+g] + a[12+g]), then vaddvq_f32.
-    float out[8];
-#pragma unroll
-    for (int c = 0; c < 2; c++)
-#pragma unroll
-      for (int ii = 0; ii < 4; ii++) {
-        float s4[4];
-#pragma unroll
-        for (int g = 0; g < 4; g++)
-          s4[g] = (acc[c][g][ii] + acc[c][g][8 + ii]) + (acc[c][g][4 + ii] + acc[c][g][12 + ii]);
-        out[4 * c + ii] = (s4[0] + s4[1]) + (s4[2] + s4[3]);
-      }
-    dot_store8<false>(X, W, b, N, M, K, np, tail, np == K && n0 + kMT <= N && m0 + kMT <= M, out, ep, pre, gtab, Y,
-               orow, ocol);
-    if (!has_next) break;
-    t = tn;
-    b = b_;
-    nt = nt_;
-    mt = mt_;
-    n0 = nn0;
-    m0 = nm0;
-    bx = nbx;
-    bw = nbw;
-  }
-}
-
 constexpr int kDotLds = kDotStageFloats * (int)sizeof(float);                     // 135,168 bytes
 constexpr int kDotLdsGelu = kDotLds + kPolyWords * (int)sizeof(double);            // 147,456 bytes
 static_assert(kDotStageFloats % 4 == 0, "the gelu table starts 16-byte aligned");
 static_assert(8 * 8 * 4 * 64 <= 4 * kMT * kLS, "dot_mfma8_k's epilogue exchange fits the LDS");
-constexpr int64_t kPersistStages = 4;
 
 // ---- soft_max ---------------------------------------------------------------------
 //
@@ -1719,8 +1542,6 @@ ArrayP dot_ggml(const DotOperand &lhs, const DotOperand &rhs, int64_t B, int64_t
     }
     static const bool lds_ok = [] {  // 135 KB of dynamic LDS, above the 64 KB default
 #define DOT_ATTR(a, c)                                                                                       \
-  SHLO_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(&dot_mfma16p_k<a, c>),                       \
-                               hipFuncAttributeMaxDynamicSharedMemorySize, kDotLdsGelu));                       \
   SHLO_HIP(hipFuncSetAttribute(reinterpret_cast<const void *>(&dot_mfma8_k<a, c>),                         \
                                hipFuncAttributeMaxDynamicSharedMemorySize, kDotLdsGelu));
       DOT_ATTR(kLoadRowVec, kLoadRowVec) DOT_ATTR(kLoadRowVec, kLoadColVec) DOT_ATTR(kLoadRowVec, kLoadScalar)
@@ -1729,7 +1550,6 @@ ArrayP dot_ggml(const DotOperand &lhs, const DotOperand &rhs, int64_t B, int64_t
       DOT_ATTR(kLoadRowVec, kLoadColQuad) DOT_ATTR(kLoadColQuad, kLoadRowVec) DOT_ATTR(kLoadColQuad, kLoadColQuad)
       DOT_ATTR(kLoadColQuad, kLoadColVec) DOT_ATTR(kLoadColVec, kLoadColQuad) DOT_ATTR(kLoadColQuad, kLoadScalar)
       DOT_ATTR(kLoadScalar, kLoadColQuad)
-      DOT_ATTR(kLoadRowVecB, kLoadRowVecB) DOT_ATTR(kLoadRowVecB, kLoadColQuadB)
       DOT_ATTR(kLoadColQuadB, kLoadRowVecB) DOT_ATTR(kLoadColQuadB, kLoadColQuadB)
 #undef DOT_ATTR
       return true;
@@ -1739,18 +1559,16 @@ ArrayP dot_ggml(const DotOperand &lhs, const DotOperand &rhs, int64_t B, int64_t
     if (tiles_m64 > 0x7FFFFFFF || tiles_n64 > 0x7FFFFFFF || tiles_m64 * tiles_n64 > 0x7FFFFFFF)
       fail("dot_general: too many output tiles");
     const int tiles_m = (int)tiles_m64;
-    const int64_t tiles_b = tiles_n64 * tiles_m64, tiles = B * tiles_b;
-    // Short contractions (up to kPersistStages stages of 128) run the
-    // persistent 16x16-layout kernel, whose next tile's loads hide under this
-    // tile's epilogue; long ones one workgroup per tile (config 3, K = 4096:
-    // 5.16 ms against 5.44 persistent).
-    // An lhs along k with an rhs along its free dim, every read in range,
-    // loads both operands straight into LDS, one workgroup per tile, at any
-    // stage count (the denoiser's K = 256 and 512 products: 6.11 -> 5.57 ms
-    // against the persistent kernel).
-    // Both operands along k in stages of 64 (Q K^T with K = 64) go straight
-    // into LDS as well.
-    const int64_t stages = (K / 16 + kKC / 16 - 1) / (kKC / 16);
+    const int64_t tiles_b = tiles_n64 * tiles_m64;
+    // One workgroup per tile.  An lhs along k with an rhs along its free dim
+    // or along k, every read in range, loads both operands straight into LDS
+    // (dot_mfma8d_k; both along k also in stages of 64, as Q K^T with K = 64);
+    // any other layout stages them through registers (dot_mfma8_k).  A
+    // persistent kernel walking tiles with the next tile's loads under this
+    // tile's epilogue was slower in every case measured (the denoiser's
+    // K = 256 and 512 products 6.11 against 5.57 ms, its [8192,512] x
+    // [512,263] output projection 64 against 57 us, config 3 5.44 against
+    // 5.16 ms).
     int dkc = 0;
     if (lx == kLoadRowVecB && (lw == kLoadColQuadB || lw == kLoadRowVecB)) {
       dkc = kKC;
@@ -1760,17 +1578,13 @@ ArrayP dot_ggml(const DotOperand &lhs, const DotOperand &rhs, int64_t B, int64_t
       lx = lw = kLoadRowVecB;
     }
     const bool direct = dkc > 0;
-    const bool persist = stages <= kPersistStages && !direct;
-    // Short direct contractions: four-wave workgroups on 32 x 64 tiles, two per CU.
+    // Short direct contractions: four-wave workgroups on 32 x 64 tiles, three per CU.
     const bool small = direct && K <= 512;
     const unsigned glds = ep.gelu ? kPolyWords * (unsigned)sizeof(double) : 0;  // the eight-wave direct kernel's dynamic LDS
     const dim3 grid_s((unsigned)(tiles_n64 * 2 * tiles_m64), (unsigned)B);
     const unsigned lds = ep.gelu ? kDotLdsGelu : kDotLds;
-    const unsigned grid = (unsigned)std::min<int64_t>(tiles, device_props().multiProcessorCount);  // one per CU
-    TileWalk tw{tiles, (int)tiles_n64, tiles_m, (int)(grid / tiles_b), (int)((grid % tiles_b) / tiles_m64),
-                (int)(grid % tiles_m64)};
     const dim3 grid1((unsigned)tiles_b, (unsigned)B);
-    if (!persist && (small ? 2 * tiles_b : tiles_b) > 0x7FFFFFFF) fail("dot_general: too many output tiles");
+    if ((small ? 2 * tiles_b : tiles_b) > 0x7FFFFFFF) fail("dot_general: too many output tiles");
     const int tl = tail;
     launch([=](hipStream_t s) {
       (void)kl, (void)kr, (void)ek;
@@ -1792,8 +1606,7 @@ ArrayP dot_ggml(const DotOperand &lhs, const DotOperand &rhs, int64_t B, int64_t
       }
 #define DOT_CASE(a, c)                                                                    \
   if (lx == a && lw == c) {                                                               \
-    if (persist) dot_mfma16p_k<a, c><<<grid, 512, lds, s>>>(X, W, N, M, K, tl, tw, ep, Y);               \
-    else dot_mfma8_k<a, c><<<grid1, 512, lds, s>>>(X, W, N, M, K, tl, tiles_m, ep, Y);                      \
+    dot_mfma8_k<a, c><<<grid1, 512, lds, s>>>(X, W, N, M, K, tl, tiles_m, ep, Y);         \
     return;                                                                               \
   }
       DOT_CASE(kLoadRowVec, kLoadRowVec) DOT_CASE(kLoadRowVec, kLoadColVec) DOT_CASE(kLoadRowVec, kLoadScalar)
@@ -1802,7 +1615,6 @@ ArrayP dot_ggml(const DotOperand &lhs, const DotOperand &rhs, int64_t B, int64_t
       DOT_CASE(kLoadRowVec, kLoadColQuad) DOT_CASE(kLoadColQuad, kLoadRowVec) DOT_CASE(kLoadColQuad, kLoadColQuad)
       DOT_CASE(kLoadColQuad, kLoadColVec) DOT_CASE(kLoadColVec, kLoadColQuad) DOT_CASE(kLoadColQuad, kLoadScalar)
       DOT_CASE(kLoadScalar, kLoadColQuad)
-      DOT_CASE(kLoadRowVecB, kLoadRowVecB) DOT_CASE(kLoadRowVecB, kLoadColQuadB)
       DOT_CASE(kLoadColQuadB, kLoadRowVecB) DOT_CASE(kLoadColQuadB, kLoadColQuadB)
 #undef DOT_CASE
     });
