@@ -638,6 +638,26 @@ typedef const volatile __attribute__((address_space(3))) float lds_f32;
 __device__ __forceinline__ float ld1_lds_v(const float *p) { return *(lds_f32 *)(p); }
 typedef const __attribute__((address_space(3))) float lds_f32n;
 
+// MI355X hands the workgroups of a launch to its 8 XCDs in turn (linear id
+// mod 8), and each XCD has its own 4 MB L2.  Consecutive tiles share operand
+// strips (a row of tiles reads one lhs strip; a batch's tiles read one pair of
+// operands), so renumber: XCD x takes the x-th contiguous run of ids, in
+// order.  The runs are [x(q+1), (x+1)(q+1)) for x < r and r(q+1) + (x-r)q
+// onward for the rest (q = total / 8, r = total % 8), which cover [0, total)
+// once each: the set of tiles computed, and every output's bits, are
+// unchanged.  Grids of 2^32 workgroups or more keep launch order.
+constexpr uint32_t kXcds = 8;
+__device__ __forceinline__ void xcd_tile(uint32_t &tx, uint32_t &ty) {
+  const uint64_t total64 = (uint64_t)gridDim.x * gridDim.y;
+  if (total64 > 0xFFFFFFFFull) return;
+  const uint32_t gx = gridDim.x, total = (uint32_t)total64;
+  const uint32_t lin = tx + gx * ty;
+  const uint32_t q = total / kXcds, r = total % kXcds, x = lin % kXcds, i = lin / kXcds;
+  const uint32_t id = (x < r ? x * (q + 1) : r * (q + 1) + (x - r) * q) + i;
+  tx = id % gx;
+  ty = id / gx;
+}
+
 template <int LX, int LW, int KC, int WAVES>
 __global__ void __launch_bounds__(WAVES * 64, 2) dot_mfma8d_k(MfmaOperand X, MfmaOperand W, int64_t N, int64_t M,
                                                            int64_t K, int tiles_m, Epilogue ep,
@@ -662,8 +682,17 @@ __global__ void __launch_bounds__(WAVES * 64, 2) dot_mfma8d_k(MfmaOperand X, Mfm
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int quad = wave % (WAVES / 2), rh = wave / (WAVES / 2);
   const int wn = WAVES == 8 ? quad >> 1 : 0, wm = WAVES == 8 ? quad & 1 : quad;
-  const int64_t b = blockIdx.y;
-  const int64_t n0 = (int64_t)(blockIdx.x / tiles_m) * TN, m0 = (int64_t)(blockIdx.x % tiles_m) * kMT;
+  // Batched four-wave launches (per-head products such as Q K^T and P V, whose
+  // operands per batch are small) renumber their workgroups so that each XCD
+  // walks whole batches (xcd_tile).  An unbatched one keeps launch order: each
+  // XCD then takes every 8th column tile, so it keeps only an eighth of the rhs
+  // hot in its L2 instead of all of it.  The eight-wave form (long
+  // contractions) keeps launch order too, in which all XCDs share one batch's
+  // operands in the MALL.
+  uint32_t tx = blockIdx.x, ty = blockIdx.y;
+  if (WAVES == 4 && gridDim.y > 1) xcd_tile(tx, ty);
+  const int64_t b = ty;
+  const int64_t n0 = (int64_t)(tx / tiles_m) * TN, m0 = (int64_t)(tx % tiles_m) * kMT;
   const int nst = (int)(K / KC);  // every stage full (the host checks)
 
   const int64_t nl = n0 + wn * 32 + 4 * (lane >> 5) + 16 * rh, ml = m0 + wm * 32 + (lane & 31);

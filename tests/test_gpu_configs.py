@@ -125,14 +125,17 @@ def test_dot_many_tiles(oracle, B, N, M, K):
 
 
 @pytest.mark.parametrize("B,N,M,K", [(2, 128, 192, 640), (1, 192, 128, 768), (3, 64, 64, 1152),
-                                     (5, 512, 512, 128), (3, 512, 704, 384), (1, 128, 64, 256)])
+                                     (5, 512, 512, 128), (3, 512, 704, 384), (1, 128, 64, 256),
+                                     (3, 64, 64, 128), (7, 64, 192, 256)])
 def test_dot_direct_lds_loads(oracle, B, N, M, K):
     """Contractions in full stages of 128 with the lhs read along k, the rhs
     along its free dim and rows multiples of 64: both operands go from HBM
     straight into LDS.  Per-tile kernel with odd and even stage counts (5, 6,
     9); persistent kernel walking more tiles than CUs with 1 and 3 stages per
-    tile (the stage buffers alternate across tile boundaries) and with 2.  Both
-    flavours, eager and compiled."""
+    tile (the stage buffers alternate across tile boundaries) and with 2.
+    Batched short contractions renumber their workgroups across the 8 XCDs:
+    (3,64,64,128) has 6 workgroups (fewer than XCDs) and (7,64,192,256) 42
+    (runs of 6 and 5).  Both flavours, eager and compiled."""
     import shlo_hip
     lhs, st = oracle.fill_normal(37, 1.0, B * N * K)
     rhs, _ = oracle.fill_normal(37, 1.0, B * K * M, state=st)
@@ -161,12 +164,13 @@ def dot_nt_module(B, N, M, K):
 
 
 @pytest.mark.parametrize("B,N,M,K", [(2, 128, 192, 64), (3, 192, 128, 192), (8, 256, 320, 64),
-                                     (2, 128, 128, 256), (1, 64, 64, 640)])
+                                     (2, 128, 128, 256), (1, 64, 64, 640), (5, 64, 64, 64)])
 def test_dot_direct_lds_loads_both_along_k(oracle, B, N, M, K):
     """Both operands contiguous along k, rows multiples of 64: straight into
     LDS in stages of 64 (K = 64, 192; the second with three stages) or of 128
-    (K = 256, 640), the rhs stored and read as the lhs.  Both flavours, eager
-    and compiled."""
+    (K = 256, 640), the rhs stored and read as the lhs.  The batched short ones
+    renumber their workgroups across the 8 XCDs: (3,192,128,192) has 36 (runs
+    of 5 and 4), (5,64,64,64) 10.  Both flavours, eager and compiled."""
     import shlo_hip
     lhs, st = oracle.fill_normal(41, 1.0, B * N * K)
     rhs, _ = oracle.fill_normal(41, 1.0, B * M * K, state=st)
