@@ -130,9 +130,9 @@ def test_dot_many_tiles(oracle, B, N, M, K):
 def test_dot_direct_lds_loads(oracle, B, N, M, K):
     """Contractions in full stages of 128 with the lhs read along k, the rhs
     along its free dim and rows multiples of 64: both operands go from HBM
-    straight into LDS.  Per-tile kernel with odd and even stage counts (5, 6,
-    9); persistent kernel walking more tiles than CUs with 1 and 3 stages per
-    tile (the stage buffers alternate across tile boundaries) and with 2.
+    straight into LDS.  Long contractions with odd and even stage counts (5,
+    6, 9); short ones (four-wave kernel) with more tiles than CUs and 1, 2 and
+    3 stages per tile.
     Batched short contractions renumber their workgroups across the 8 XCDs:
     (3,64,64,128) has 6 workgroups (fewer than XCDs) and (7,64,192,256) 42
     (runs of 6 and 5).  Both flavours, eager and compiled."""

@@ -181,7 +181,7 @@ def test_attention_scale_and_mask(oracle, S, K):
 @pytest.mark.parametrize("N,K,M", [(256, 64, 192), (130, 512, 70), (64, 1024, 128), (33, 17, 9)])
 def test_bias_and_residual(oracle, N, K, M):
     """x W + bias (broadcast over rows), then a residual on the left (rev):
-    the persistent kernel (K <= 512), the per-tile kernel, partial tiles and
+    the four-wave kernel (K <= 512), the eight-wave kernel, partial tiles and
     row tails."""
     bias = normal(oracle, 9, (M,), 0.5)
     res = normal(oracle, 10, (N, M))
@@ -280,8 +280,8 @@ def test_planted_faults_still_differ(oracle):
 @pytest.mark.parametrize("N,K,M", [(256, 512, 192), (130, 1024, 70), (128, 1024, 128), (33, 33, 9), (64, 16, 64)])
 def test_bias_then_gelu(oracle, N, K, M):
     """x W + bias, then ggml.gelu_erf (the FFN's first projection): the
-    correctly rounded erff runs in the product's epilogue from a table in LDS;
-    the persistent kernel, the per-tile kernel, partial tiles and tails."""
+    correctly rounded erff runs in the product's epilogue (table in LDS, or read through the cache in the four-wave kernel);
+    the four-wave and eight-wave kernels, partial tiles and tails."""
     bias = normal(oracle, 60, (M,), 0.5)
     check(oracle, Chain((), N, K, M, [("add", bias, ("bcast", (1,)), False), ("gelu", None, None, False)]))
 
