@@ -59,7 +59,7 @@ shlo::Shape shape_of(const int64_t *s, size_t rank) {
 }
 
 // Scalar parameters of a kernel_apply: the u32 words of the last input
-// (Run.lean:140-145), read from its host shadow when it has one.
+// (Run.lean:51-52), read from its host shadow when it has one.
 std::vector<uint32_t> params_of(const shlo::ArrayP &p) {
   std::vector<uint8_t> bytes;
   if (!p->shadow.empty() && p->contiguous()) {
@@ -231,7 +231,7 @@ int shlo_kernel_apply(const shlo_kernel *k, const shlo_arr *const *inputs, size_
       if (in.size() != c) fail(strf("%s takes %zu inputs, got %zu", n.c_str(), c, in.size()));
     };
     ArrayP y;
-    if (n == "mul_mat") {  // Run.lean:155-158: [w, x, p = K, M, R, wBatchStride, N, plain]
+    if (n == "mul_mat") {  // Run.lean:64-65: [w, x, p = K, M, R, wBatchStride, N, plain]
       want(3);
       auto p = params_of(in[2]);
       y = mul_mat(in[0], in[1], p[0], p[1], p[2], p[4], p[3], p[5] ? (int)kTailPlain : default_dot_tail());
@@ -521,6 +521,14 @@ int shlo_device_info(char *name, size_t cap, int *cus, uint64_t *pool_bytes) {
     }
     if (cus) *cus = p.multiProcessorCount;
     if (pool_bytes) *pool_bytes = shlo::pool_reserved_bytes();
+  });
+}
+
+int shlo_last_dot_kernel(char *name, size_t cap) {
+  return guard("last_dot_kernel", [&] {
+    need(name, "name");
+    if (!cap) shlo::fail("cap must be at least 1");
+    snprintf(name, cap, "%s", shlo::last_dot_kernel().c_str());
   });
 }
 

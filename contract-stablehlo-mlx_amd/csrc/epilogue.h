@@ -18,7 +18,7 @@
 namespace shlo {
 
 // Binary32 semantics of the arithmetic binary op codes
-// (StablehloMlx/Mlx.lean:286-307): maximum / minimum order -0 below +0
+// (StablehloMlx/Mlx.lean:88-108): maximum / minimum order -0 below +0
 // (mx::maximum).  A NaN operand propagates as on arm64 and x86 (the first
 // NaN operand, quieted, sign kept): the result is x + y, which the GPU's add
 // returns that way, where its subtract would flip a NaN's sign.

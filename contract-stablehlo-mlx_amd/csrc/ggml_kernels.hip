@@ -1502,8 +1502,15 @@ unsigned grid_cap(int64_t n, int block, int64_t cap) {
 
 namespace {
 int g_default_tail = kTailStock;
+std::string g_last_dot = "";  // the kernel the last dot_ggml call chose
+
+const char *loader_name(int l) {
+  static const char *const n[] = {"RowVec", "ColVec", "Scalar", "ColQuad", "RowVecB", "ColQuadB"};
+  return l >= 0 && l < 6 ? n[l] : "?";
 }
+}  // namespace
 int default_dot_tail() { return g_default_tail; }
+const std::string &last_dot_kernel() { return g_last_dot; }
 void set_default_dot_tail(int t) {
   if (t != kTailStock && t != kTailPinned) fail("flavor: 0 (stock) or 1 (pinned)");
   g_default_tail = t;
@@ -1598,8 +1605,10 @@ ArrayP dot_ggml(const DotOperand &lhs, const DotOperand &rhs, int64_t B, int64_t
     // K = 256 and 512 products 6.11 against 5.57 ms, its [8192,512] x
     // [512,263] output projection 64 against 57 us, config 3 5.44 against
     // 5.16 ms).
+    // The direct kernel has no serial tail: it needs K a whole number of
+    // stages (the buffer loaders alone only need whole stages of blocks).
     int dkc = 0;
-    if (lx == kLoadRowVecB && (lw == kLoadColQuadB || lw == kLoadRowVecB)) {
+    if (lx == kLoadRowVecB && (lw == kLoadColQuadB || lw == kLoadRowVecB) && K % kKC == 0) {
       dkc = kKC;
     } else if (lx == kLoadRowVec && lw == kLoadRowVec && K % 64 == 0 && K >= 64 && ln % 4 == 0 && rm % 4 == 0 &&
                in_range(ln, lk, lb, N) && in_range(rm, rk, rb, M)) {
@@ -1607,6 +1616,25 @@ ArrayP dot_ggml(const DotOperand &lhs, const DotOperand &rhs, int64_t B, int64_t
       lx = lw = kLoadRowVecB;
     }
     const bool direct = dkc > 0;
+    // The register-staged kernel is instantiated with the buffer loaders only
+    // for a column-read lhs: a row-read lhs that did not go direct takes the
+    // plain loaders (same elements, bounds-checked addressing).
+    if (!direct && lx == kLoadRowVecB) {
+      lx = kLoadRowVec;
+      lw = lw == kLoadRowVecB ? (int)kLoadRowVec : (int)kLoadColQuad;
+    }
+    if (!direct) {
+      static const int kCases[][2] = {
+          {kLoadRowVec, kLoadRowVec},   {kLoadRowVec, kLoadColVec},     {kLoadRowVec, kLoadScalar},
+          {kLoadColVec, kLoadRowVec},   {kLoadColVec, kLoadColVec},     {kLoadColVec, kLoadScalar},
+          {kLoadScalar, kLoadRowVec},   {kLoadScalar, kLoadColVec},     {kLoadScalar, kLoadScalar},
+          {kLoadRowVec, kLoadColQuad},  {kLoadColQuad, kLoadRowVec},    {kLoadColQuad, kLoadColQuad},
+          {kLoadColQuad, kLoadColVec},  {kLoadColVec, kLoadColQuad},    {kLoadColQuad, kLoadScalar},
+          {kLoadScalar, kLoadColQuad},  {kLoadColQuadB, kLoadRowVecB}, {kLoadColQuadB, kLoadColQuadB}};
+      bool have = false;
+      for (auto &c : kCases) have |= c[0] == lx && c[1] == lw;
+      if (!have) fail(strf("dot_general: no kernel for loaders %s, %s", loader_name(lx), loader_name(lw)));
+    }
     // Short direct contractions: four-wave workgroups on 32 x 64 tiles, three per CU.
     const bool small = direct && K <= 512;
     const unsigned glds = ep.gelu ? kPolyWords * (unsigned)sizeof(double) : 0;  // the eight-wave direct kernel's dynamic LDS
@@ -1615,6 +1643,10 @@ ArrayP dot_ggml(const DotOperand &lhs, const DotOperand &rhs, int64_t B, int64_t
     const dim3 grid1((unsigned)tiles_b, (unsigned)B);
     if ((small ? 2 * tiles_b : tiles_b) > 0x7FFFFFFF) fail("dot_general: too many output tiles");
     const int tl = tail;
+    if (direct)
+      g_last_dot = strf("dot_mfma8d_k<RowVecB,%s,%d,%d>", loader_name(lw), small ? 64 : dkc, small ? 4 : 8);
+    else
+      g_last_dot = strf("dot_mfma8_k<%s,%s>", loader_name(lx), loader_name(lw));
     launch([=](hipStream_t s) {
       (void)kl, (void)kr, (void)ek;
       if (direct && small) {
@@ -1650,6 +1682,7 @@ ArrayP dot_ggml(const DotOperand &lhs, const DotOperand &rhs, int64_t B, int64_t
     return y;
   }
   const unsigned grid = grid_cap(n_out, 256, 1 << 20);
+  g_last_dot = strf("dot_ggml_simple<%s>", tail == kTailStock ? "stock" : tail == kTailPinned ? "pinned" : "plain");
   launch([=](hipStream_t s) {
     (void)kl, (void)kr, (void)ek;
     switch (tail) {

@@ -1,18 +1,18 @@
 // Array operations: the MI355X counterparts of the mlx-c calls the reference
 // shim makes (c/smlx_shim.c:142-264, :301-323, :388-414) and of the exact
-// kernels its Run.lean dispatches (StablehloMlx/Kernels/Run.lean:155-197).
+// kernels its Run.lean dispatches (StablehloMlx/Kernels/Run.lean:64-104).
 #pragma once
 
 #include "runtime.h"
 
 namespace shlo {
 
-// Unary op codes (StablehloMlx/Mlx.lean:274-285).
+// Unary op codes (StablehloMlx/Mlx.lean:76-87).
 enum UnaryOp : uint32_t {
   kNeg = 0, kAbs = 1, kSqrt = 2, kFloor = 3, kExp = 4, kErf = 5, kNot = 6,
   kInvert = 7, kRsqrt = 8, kTanh = 9, kSigmoid = 10
 };
-// Binary op codes (StablehloMlx/Mlx.lean:286-307).
+// Binary op codes (StablehloMlx/Mlx.lean:88-108).
 enum BinaryOp : uint32_t {
   kAdd = 0, kSub = 1, kMul = 2, kDiv = 3, kMax = 4, kMin = 5, kAnd = 6, kOr = 7,
   kXor = 8, kShl = 9, kShr = 10, kEq = 11, kNe = 12, kLt = 13, kLe = 14, kGt = 15,
@@ -94,7 +94,11 @@ struct FusedOp {
 ArrayP dot_ggml(const DotOperand &lhs, const DotOperand &rhs, int64_t B, int64_t N, int64_t M,
                 int64_t K, int tail, const std::vector<FusedOp> &epi = {});
 
-// The reference's Run.mulMat surface (Run.lean:155-158): w rows of K, x rows
+// The kernel the last dot_ggml call chose, e.g. "dot_mfma8d_k<RowVecB,ColQuadB,128,8>"
+// (host bookkeeping for tests and profiles; "" before the first call).
+const std::string &last_dot_kernel();
+
+// The reference's Run.mulMat surface (Run.lean:64-65): w rows of K, x rows
 // of K; y[r*M + m] = dot(w row (r/N)*wBatchStride/K + m, x row r).
 ArrayP mul_mat(const ArrayP &w, const ArrayP &x, int64_t K, int64_t M, int64_t R, int64_t N,
                int64_t wBatchStride, int tail);

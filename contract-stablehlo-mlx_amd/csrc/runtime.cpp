@@ -225,14 +225,13 @@ ArrayP array_from_host(const void *data, size_t nbytes, const Shape &shape, uint
   auto a = new_array(dtype, shape);
   if (a->nbytes() != nbytes) fail("ofBytes: byte count does not match the shape");
   if (nbytes) {
-    if (g_trace) {
-      // Constants made while tracing are uploaded once, now; the graph only
-      // reads them.
-      SHLO_HIP(hipMemcpy(a->data(), data, nbytes, hipMemcpyHostToDevice));
-    } else {
-      SHLO_HIP(hipMemcpyAsync(a->data(), data, nbytes, hipMemcpyHostToDevice, stream()));
-      SHLO_HIP(hipStreamSynchronize(stream()));
-    }
+    // Ordered on the executor's stream: the pool may hand out a block that a
+    // kernel queued earlier on that stream still writes (the stream is
+    // non-blocking, so a copy on the null stream would not wait for it).
+    // Constants made while tracing are uploaded once, here, outside the
+    // recorded launches; the graph only reads them.
+    SHLO_HIP(hipMemcpyAsync(a->data(), data, nbytes, hipMemcpyHostToDevice, stream()));
+    SHLO_HIP(hipStreamSynchronize(stream()));
   }
   if (nbytes <= Array::kShadowBytes) a->shadow.assign((const uint8_t *)data, (const uint8_t *)data + nbytes);
   return a;

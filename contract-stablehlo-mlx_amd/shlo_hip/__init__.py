@@ -41,7 +41,7 @@ _NP = {BOOL: np.bool_, U8: np.uint8, U16: np.uint16, U32: np.uint32, U64: np.uin
        I16: np.int16, I32: np.int32, I64: np.int64, F16: np.float16, F32: np.float32, F64: np.float64}
 _FROM_NP = {np.dtype(v): k for k, v in _NP.items()}
 
-# Unary and binary op codes (StablehloMlx/Mlx.lean:274-307)
+# Unary and binary op codes (StablehloMlx/Mlx.lean:76-108)
 UNARY = dict(neg=0, abs=1, sqrt=2, floor=3, exp=4, erf=5, not_=6, invert=7, rsqrt=8, tanh=9, sigmoid=10)
 BINARY = dict(add=0, sub=1, mul=2, div=3, max=4, min=5, and_=6, or_=7, xor=8, shl=9, shr=10, eq=11, ne=12,
               lt=13, le=14, gt=15, ge=16, matmul=17, rem=18, land=19, lor=20)
@@ -293,7 +293,7 @@ class Kernel:
 
 
 def u32_arr(words) -> Arr:
-    """Kernel parameters, padded to 8 words (Run.lean:140-145)."""
+    """Kernel parameters, padded to 8 words (Run.lean:51-52)."""
     w = list(words) + [0] * (8 - len(words))
     return from_numpy(np.array(w, dtype=np.uint32))
 
@@ -469,6 +469,14 @@ def device_info():
     pool = ctypes.c_uint64()
     _check(_lib.shlo_device_info(name, _SZ(256), ctypes.byref(cus), ctypes.byref(pool)))
     return name.value.decode(), cus.value, pool.value
+
+
+def last_dot_kernel() -> str:
+    """The dot kernel (family and template arguments) the last dot_general
+    dispatch chose."""
+    buf = ctypes.create_string_buffer(256)
+    _check(_lib.shlo_last_dot_kernel(buf, _SZ(256)))
+    return buf.value.decode()
 
 
 def lib_handle():

@@ -70,12 +70,12 @@ int shlo_dtype(const shlo_arr *a, uint8_t *dtype);
 
 /* ---- ops: one executor op each -------------------------------------------- */
 
-/* smlx_unary (c/smlx_shim.c:148-166); op codes of StablehloMlx/Mlx.lean:274-285:
+/* smlx_unary (c/smlx_shim.c:148-166); op codes of StablehloMlx/Mlx.lean:76-87:
  * neg 0, abs 1, sqrt 2, floor 3, exp 4, erf 5, not 6, invert 7, rsqrt 8,
  * tanh 9, sigmoid 10. */
 int shlo_unary(uint32_t op, const shlo_arr *a, shlo_arr **out);
 
-/* smlx_binary (c/smlx_shim.c:168-196); op codes of StablehloMlx/Mlx.lean:286-307:
+/* smlx_binary (c/smlx_shim.c:168-196); op codes of StablehloMlx/Mlx.lean:88-108:
  * add 0, sub 1, mul 2, div 3, max 4, min 5, and 6, or 7, xor 8, shl 9, shr 10,
  * eq 11, ne 12, lt 13, le 14, gt 15, ge 16, matmul 17, rem 18, land 19, lor 20.
  * Operands broadcast (numpy rules). */
@@ -121,7 +121,7 @@ void shlo_kernel_free(shlo_kernel *k);
 
 /* smlx_kernel_apply (c/smlx_shim.c:299-323): inputs in the kernel's binding
  * order, the last one being the u32 parameter array of
- * StablehloMlx/Kernels/Run.lean:155-197 (e.g. mul_mat: [K, M, R,
+ * StablehloMlx/Kernels/Run.lean:64-104 (e.g. mul_mat: [K, M, R,
  * wBatchStride, N, plain]).  out_shapes holds the nout output shapes
  * back to back (out_ranks[i] dims each); grid and threadgroup are accepted
  * and checked for 3 entries, and the kernel picks its own launch shape.
@@ -237,6 +237,11 @@ int shlo_timer_stop(float *ms);
 int shlo_time_apply(shlo_fn *f, const shlo_arr *const *inputs, size_t nin, int reps, float *ms);
 /* Device name, compute units and the bytes the array pool holds. */
 int shlo_device_info(char *name, size_t cap, int *cus, uint64_t *pool_bytes);
+/* The kernel family and template arguments that the most recent dot_general
+ * (or mul_mat) dispatch chose, e.g. "dot_mfma8d_k<RowVecB,ColQuadB,128,8>",
+ * written NUL-terminated into name[cap] ("" before the first dispatch).  Lets
+ * tests check that a shape reaches the kernel it is meant to exercise. */
+int shlo_last_dot_kernel(char *name, size_t cap);
 /* The device address of an array's first element (for in-place interop). */
 int shlo_data_ptr(const shlo_arr *a, void **ptr);
 
