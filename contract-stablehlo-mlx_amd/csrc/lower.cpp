@@ -423,6 +423,11 @@ std::pair<int64_t, int64_t> rows_cols(const Ty &t) {  // Lower.lean:301-303
 }
 
 ArrayP convert_op(const ArrayP &a, const Ty &src, const Ty &out) {  // Lower.lean:306-315
+  // binary64 converts only to and from binary32 and to int64 (toward zero,
+  // saturating, NaN to 0), as the reference's soft-float kernels do.
+  if (src.el == "f64" && out.el != "f32" && out.el != "f64" && out.el != "i64" && out.el != "si64")
+    fail("convert f64 to " + out.el + " is not carried");
+  if (out.el == "f64" && src.el != "f32" && src.el != "f64") fail("convert " + src.el + " to f64 is not carried");
   return astype(a, el_dtype(out.el));
 }
 
@@ -531,6 +536,7 @@ struct Lowerer {
       const Block &body = o.regions[0];
       if (!(body.ops.size() == 1 && body.ops[0].name == "stablehlo.maximum" && o.operands.size() == 2))
         fail("reduce: only a single-operand maximum is carried");
+      if (el0 == "f64") fail("reduce on f64 is not carried");
       ArrayP r = args[0];
       std::sort(dims.begin(), dims.end(), std::greater<int64_t>());
       for (int64_t d : dims) r = max_axis(r, (int)d);

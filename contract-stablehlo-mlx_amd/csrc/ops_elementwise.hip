@@ -287,6 +287,74 @@ constexpr bool is_flt() {
   return std::is_same<T, float>::value || std::is_same<T, f16>::value || std::is_same<T, double>::value;
 }
 
+// ---- binary64 with the reference's NaN and conversion rules ---------------------
+//
+// The reference carries binary64 tensors as bit patterns through soft-float
+// kernels (StablehloMlx/Kernels/SoftFloat.lean) that behave as arm64 with
+// FPCR.DN clear: a NaN operand comes back quieted, sign and payload kept, the
+// first operand's when both are NaN (f64Add/f64Sub/f64Mul/f64Div,
+// SoftFloat.lean:137-259); an invalid operation (inf - inf, 0 * inf, 0 / 0,
+// inf / inf) gives the default NaN +0x7FF8000000000000.  gfx950's binary64
+// instructions round to nearest even with subnormals, as those kernels do;
+// the NaN choices are made explicit here, since the hardware's own (and the
+// compiler's freedom to commute operands) need not match them.
+constexpr uint64_t kSign64 = 0x8000000000000000ull, kQuiet64 = 0x0008000000000000ull;
+constexpr uint64_t kInf64 = 0x7FF0000000000000ull, kNan64 = 0x7FF8000000000000ull;
+__device__ __forceinline__ uint64_t d_bits(double x) { return __builtin_bit_cast(uint64_t, x); }
+__device__ __forceinline__ double bits_d(uint64_t u) { return __builtin_bit_cast(double, u); }
+__device__ __forceinline__ bool d_isnan(double x) { return (d_bits(x) & ~kSign64) > kInf64; }
+__device__ __forceinline__ double d_quiet(double x) { return bits_d(d_bits(x) | kQuiet64); }
+
+__device__ __forceinline__ double f64_binary(uint32_t op, double x, double y) {
+  if (d_isnan(x)) return d_quiet(x);
+  if (d_isnan(y)) return d_quiet(y);
+  double r;
+  switch (op) {
+    case kAdd: r = x + y; break;
+    case kSub: r = x - y; break;  // a + (-b) (f64Sub, SoftFloat.lean:197-202)
+    case kMul: r = x * y; break;
+    case kDiv: r = x / y; break;  // IEEE division (the HIP lowering is correctly rounded)
+    // maximum / minimum: -0 below +0, the first operand on a tie
+    // (f64MaxMin, Lower.lean:290-296)
+    case kMax:
+      if (x == y) return std::signbit(x) ? y : x;
+      return x > y ? x : y;
+    case kMin:
+      if (x == y) return std::signbit(x) ? x : y;
+      return x < y ? x : y;
+    case kRem: r = std::fmod(x, y); break;
+    default: return x;
+  }
+  return d_isnan(r) ? bits_d(kNan64) : r;
+}
+
+// f64ToI64 (SoftFloat.lean:219-236, arm64 fcvtzs): toward zero, saturating,
+// NaN to 0.
+__device__ __forceinline__ int64_t f64_to_i64(double x) {
+  if (d_isnan(x)) return 0;
+  if (x >= 0x1p63) return INT64_MAX;
+  if (x <= -0x1p63) return INT64_MIN;
+  return (int64_t)x;
+}
+// f64ToF32 (SoftFloat.lean:95-120): round to nearest even with binary32
+// subnormals; a NaN keeps its sign and the top of its payload, quieted.
+__device__ __forceinline__ float f64_to_f32(double x) {
+  if (d_isnan(x)) {
+    const uint64_t u = d_bits(x);
+    return __builtin_bit_cast(float, (uint32_t)((u >> 32) & 0x80000000u) | 0x7FC00000u |
+                                         (uint32_t)((u & 0x000FFFFFFFFFFFFFull) >> 29));
+  }
+  return (float)x;
+}
+// f64FromF32 (SoftFloat.lean:73-86): exact; a NaN keeps its sign and payload
+// (it is not quieted).
+__device__ __forceinline__ double f32_to_f64(float x) {
+  const uint32_t b = __builtin_bit_cast(uint32_t, x);
+  if ((b & 0x7FFFFFFFu) > 0x7F800000u)
+    return bits_d(((uint64_t)(b >> 31) << 63) | kInf64 | ((uint64_t)(b & 0x7FFFFFu) << 29));
+  return (double)x;
+}
+
 // ---- unary functors ------------------------------------------------------------
 
 template <class T>
@@ -298,9 +366,12 @@ struct UnaryF {
       const C v = (C)x;
       switch (op) {
         case kNeg: return (T)(-v);
-        case kAbs: return (T)(v < (C)0 || (v == (C)0 && std::signbit(v)) ? -v : v);
+        case kAbs: return (T)std::fabs(v);  // clears the sign bit, of a NaN too (Lower.lean:360)
         case kSqrt: return (T)std::sqrt(v);
-        case kFloor: return (T)std::floor(v);
+        case kFloor:
+          if constexpr (std::is_same<T, double>::value)  // f64Floor (SoftFloat.lean:204-217)
+            if (d_isnan(v)) return d_quiet(v);
+          return (T)std::floor(v);
         case kExp: return (T)std::exp(v);
         case kErf: return (T)std::erf(v);
         case kNot: return (T)(v == (C)0 ? 1 : 0);
@@ -329,8 +400,12 @@ struct UnaryF {
 template <class TI, class TO>
 struct CastF {
   __device__ TO operator()(TI x) const {
-    if constexpr (std::is_same<TO, uint8_t>::value && !std::is_same<TI, uint8_t>::value) {
-      return (TO)x;
+    if constexpr (std::is_same<TI, double>::value && std::is_same<TO, int64_t>::value) {
+      return f64_to_i64(x);
+    } else if constexpr (std::is_same<TI, double>::value && std::is_same<TO, float>::value) {
+      return f64_to_f32(x);
+    } else if constexpr (std::is_same<TI, float>::value && std::is_same<TO, double>::value) {
+      return f32_to_f64(x);
     } else {
       return (TO)x;
     }
@@ -351,6 +426,8 @@ struct BinaryF {
       if (op == kDivApprox) return a * __builtin_amdgcn_rcpf(b);
       if (op == kRem) return std::fmod(a, b);
       return f32_binary(op, a, b);
+    } else if constexpr (std::is_same<T, double>::value) {
+      return f64_binary(op == kDivApprox ? (uint32_t)kDiv : op, a, b);
     } else if constexpr (is_flt<T>()) {
       using C = typename std::conditional<std::is_same<T, double>::value, double, T>::type;
       const C x = (C)a, y = (C)b;

@@ -361,6 +361,93 @@ uint64_t orc_checksum_words(const uint32_t *w, size_t count, uint64_t start_inde
 	return s;
 }
 
+/* ---- binary64 on the generic path (StablehloMlx/Kernels/SoftFloat.lean) ----
+ *
+ * The reference carries f64 tensors as uint64 bit patterns through integer
+ * soft-float kernels.  Their rounding is IEEE binary64 round-to-nearest-even
+ * with subnormals, which the host's SSE2 arithmetic computes directly; what
+ * follows restates their choices for NaNs, signed zeros and conversions. */
+
+#define Q64 0x0008000000000000ull
+#define INF64 0x7FF0000000000000ull
+#define NAN64 0x7FF8000000000000ull  /* arm64's default NaN (invalid operations) */
+#define SIGN64 0x8000000000000000ull
+static inline uint64_t d2u(double d) { uint64_t u; memcpy(&u, &d, 8); return u; }
+static inline double u2d(uint64_t u) { double d; memcpy(&d, &u, 8); return d; }
+static inline int nan64(uint64_t u) { return (u & ~SIGN64) > INF64; }
+
+/* f64Add / f64Sub / f64Mul / f64Div (SoftFloat.lean:137-202, :239-259): a NaN
+ * operand comes back quieted with its sign, the first operand's when both are
+ * NaN; an invalid operation gives NAN64.  f64Floor (:204-217): exact, NaN
+ * quieted, -0 kept.  f64ToI64 (:219-236): toward zero, saturating, NaN -> 0. */
+uint64_t orc_f64_ew(int op, uint64_t a, uint64_t b) {
+	if (op == 5) {
+		if (nan64(a)) return 0;
+		const double x = u2d(a);
+		if (x >= 0x1p63) return 0x7FFFFFFFFFFFFFFFull;
+		if (x <= -0x1p63) return SIGN64;
+		return (uint64_t)(int64_t)x;
+	}
+	if (op == 4) {
+		if (nan64(a)) return a | Q64;
+		return d2u(floor(u2d(a)));
+	}
+	if (nan64(a)) return a | Q64;
+	if (nan64(b)) return b | Q64;
+	const double x = u2d(a), y = u2d(b);
+	double r;
+	switch (op) {
+	case 0: r = x + y; break;
+	case 1: r = x - y; break;
+	case 2: r = x * y; break;
+	case 3: r = x / y; break;
+	default: return 0;
+	}
+	const uint64_t u = d2u(r);
+	return nan64(u) ? NAN64 : u;
+}
+
+/* f64MaxMin (Lower.lean:290-296): a NaN operand (the first one) quieted; else
+ * the larger (smaller) in an order with -0 below +0, the first operand on a
+ * tie. */
+uint64_t orc_f64_maxmin(int is_max, uint64_t a, uint64_t b) {
+	if (nan64(a)) return a | Q64;
+	if (nan64(b)) return b | Q64;
+	/* f64Key: a uint64 whose unsigned order is the numeric order */
+	const uint64_t ka = (a >> 63) ? ~a : (a | SIGN64), kb = (b >> 63) ? ~b : (b | SIGN64);
+	return is_max ? (ka >= kb ? a : b) : (ka <= kb ? a : b);
+}
+
+/* f64FromF32 (SoftFloat.lean:73-86): exact widening; a NaN keeps its sign and
+ * payload shifted up, without setting the quiet bit. */
+uint64_t orc_f64_of_f32(uint32_t x) {
+	if ((x & 0x7FFFFFFFu) > 0x7F800000u)
+		return ((uint64_t)(x >> 31) << 63) | INF64 | ((uint64_t)(x & 0x7FFFFFu) << 29);
+	return d2u((double)u2f(x));
+}
+
+/* f64ToF32 (SoftFloat.lean:95-120): round to nearest even with binary32
+ * subnormals, overflow to infinity; a NaN keeps its sign and the top of its
+ * payload, quieted. */
+uint32_t orc_f32_of_f64(uint64_t d) {
+	if (nan64(d))
+		return (uint32_t)((d >> 32) & 0x80000000u) | 0x7FC00000u | (uint32_t)((d & 0xFFFFFFFFFFFFFull) >> 29);
+	return f2u((float)u2d(d));
+}
+
+void orc_f64_ew_n(int op, const uint64_t *a, const uint64_t *b, uint64_t *out, size_t n) {
+	for (size_t i = 0; i < n; i++) out[i] = orc_f64_ew(op, a[i], b ? b[i] : a[i]);
+}
+void orc_f64_maxmin_n(int is_max, const uint64_t *a, const uint64_t *b, uint64_t *out, size_t n) {
+	for (size_t i = 0; i < n; i++) out[i] = orc_f64_maxmin(is_max, a[i], b[i]);
+}
+void orc_f64_of_f32_n(const uint32_t *x, uint64_t *out, size_t n) {
+	for (size_t i = 0; i < n; i++) out[i] = orc_f64_of_f32(x[i]);
+}
+void orc_f32_of_f64_n(const uint64_t *x, uint32_t *out, size_t n) {
+	for (size_t i = 0; i < n; i++) out[i] = orc_f32_of_f64(x[i]);
+}
+
 /* ---- fixture writer: the case table of ref/ggml_ref.c:152-295 ------------- */
 
 struct tensor { int64_t ne[4]; float *d; };

@@ -114,6 +114,27 @@ void orc_expf_range(uint32_t base, uint32_t count, uint32_t *out, int nthreads);
  * 256 chunks of the exhaustive erff sweep in a small committed fixture. */
 uint64_t orc_checksum_words(const uint32_t *w, size_t count, uint64_t start_index);
 
+/* ---- binary64 on the generic path --------------------------------------- */
+
+/* The reference's soft-float binary64 (StablehloMlx/Kernels/SoftFloat.lean),
+ * on bit patterns.  op: 0 add, 1 subtract, 2 multiply, 3 divide, 4 floor of
+ * a, 5 a to int64 (the f64_ew op codes, Run.lean:87-92).  Rounding is the
+ * host's IEEE binary64; the NaN, signed-zero and saturation rules are the
+ * reference's.  Pinned by exact rational arithmetic (Python Fraction,
+ * correctly rounded back) on random, subnormal and boundary operands, and by
+ * the special cases SoftFloat.lean states (tests/test_oracle_f64.py). */
+uint64_t orc_f64_ew(int op, uint64_t a, uint64_t b);
+/* maximum (is_max) / minimum of binary64 (Lower.lean:290-296). */
+uint64_t orc_f64_maxmin(int is_max, uint64_t a, uint64_t b);
+/* binary32 -> binary64 and back (SoftFloat.lean:73-86, :95-120). */
+uint64_t orc_f64_of_f32(uint32_t x);
+uint32_t orc_f32_of_f64(uint64_t d);
+/* Element-wise forms over n values (b may be NULL for ops 4 and 5). */
+void orc_f64_ew_n(int op, const uint64_t *a, const uint64_t *b, uint64_t *out, size_t n);
+void orc_f64_maxmin_n(int is_max, const uint64_t *a, const uint64_t *b, uint64_t *out, size_t n);
+void orc_f64_of_f32_n(const uint32_t *x, uint64_t *out, size_t n);
+void orc_f32_of_f64_n(const uint64_t *x, uint32_t *out, size_t n);
+
 /* ---- the fixture generator's cases (ref/ggml_ref.c:152-283) ------------- */
 
 /* Writes <outdir>/<case>/in<i>.f32, out.f32, meta.txt for one case, in the

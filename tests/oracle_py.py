@@ -31,6 +31,8 @@ _l.orc_checksum_words.restype = ctypes.c_uint64
 _l.orc_checksum_words.argtypes = [_P, ctypes.c_size_t, ctypes.c_uint64]
 _l.orc_write_case.argtypes = [ctypes.c_char_p, ctypes.c_char_p, ctypes.c_int]
 _l.orc_case_name.restype = ctypes.c_char_p
+_l.orc_f64_ew.restype = ctypes.c_uint64
+_l.orc_f64_ew.argtypes = [ctypes.c_int, ctypes.c_uint64, ctypes.c_uint64]
 
 TAIL_STOCK, TAIL_PINNED, TAIL_PLAIN = 0, 1, 2
 NCPU = min(os.cpu_count() or 1, 16)
@@ -134,6 +136,43 @@ def erff_range(base, count, nthreads=NCPU):
 def checksum_words(words, start_index):
     w = np.ascontiguousarray(words, np.uint32)
     return int(_l.orc_checksum_words(_ptr(w), ctypes.c_size_t(w.size), ctypes.c_uint64(start_index)))
+
+
+def _u64(a):
+    return np.ascontiguousarray(np.asarray(a).view(np.uint64) if np.asarray(a).dtype == np.float64
+                                else np.asarray(a, np.uint64))
+
+
+def f64_ew(op, a, b=None):
+    """The reference's soft-float binary64 op (0 add, 1 sub, 2 mul, 3 div,
+    4 floor, 5 to int64) on arrays of bit patterns (uint64) or float64;
+    returns uint64 bit patterns."""
+    a = _u64(a)
+    bb = None if b is None else _u64(b)
+    out = np.empty(a.shape, np.uint64)
+    _l.orc_f64_ew_n(ctypes.c_int(op), _ptr(a), None if bb is None else _ptr(bb), _ptr(out), ctypes.c_size_t(a.size))
+    return out
+
+
+def f64_maxmin(is_max, a, b):
+    a, b = _u64(a), _u64(b)
+    out = np.empty(a.shape, np.uint64)
+    _l.orc_f64_maxmin_n(ctypes.c_int(int(is_max)), _ptr(a), _ptr(b), _ptr(out), ctypes.c_size_t(a.size))
+    return out
+
+
+def f64_of_f32(x):
+    x = np.ascontiguousarray(np.asarray(x, np.float32).view(np.uint32))
+    out = np.empty(x.shape, np.uint64)
+    _l.orc_f64_of_f32_n(_ptr(x), _ptr(out), ctypes.c_size_t(x.size))
+    return out
+
+
+def f32_of_f64(d):
+    d = _u64(d)
+    out = np.empty(d.shape, np.uint32)
+    _l.orc_f32_of_f64_n(_ptr(d), _ptr(out), ctypes.c_size_t(d.size))
+    return out
 
 
 def case_names():

@@ -47,9 +47,9 @@ def test_attention_chain_vs_oracle(oracle, shape):
         assert not same_bits(got, want), fault
 
 
-def test_attention_config4_graph_equals_eager_and_one_head(oracle):
-    """B=8, H=8, S=512, D=64: graph == eager on the whole output, and one
-    (batch, head) slice against the oracle."""
+def test_attention_config4_all_heads_vs_oracle(oracle):
+    """B=8, H=8, S=512, D=64: graph == eager on the whole
+    output, and every (batch, head) against the oracle."""
     import shlo_hip
     from shlo_hip import configs
     B, H, S, D = 8, 8, 512, 64
@@ -59,28 +59,34 @@ def test_attention_config4_graph_equals_eager_and_one_head(oracle):
     g = m.prepare(0, True).call(ins)[0].numpy()
     e = m.prepare(0, False).call(ins)[0].numpy()
     assert same_bits(g, e)
-    bh = (5, 3)
-    one = attention_oracle(oracle, q[bh[0]:bh[0] + 1, bh[1]:bh[1] + 1], k[bh[0]:bh[0] + 1, bh[1]:bh[1] + 1],
-                           v[bh[0]:bh[0] + 1, bh[1]:bh[1] + 1], mask)
-    assert same_bits(g[bh[0], bh[1]], one[0, 0])
+    want = attention_oracle(oracle, q, k, v, mask)
+    assert same_bits(g, want)
 
 
-def test_dot_config3_slices_vs_oracle(oracle):
-    """Batched [16,1024,4096] x [16,4096,4096]: two output rows of two batches
-    against the oracle (full-size operands on the GPU)."""
+def test_dot_config3_strips_vs_oracle(oracle):
+    """Batched [16,1024,4096] x [16,4096,4096] against the
+    oracle on whole tiles: the first 64-row strip (every column tile) of
+    batches 0 and 11, the last 64-row strip of batch 15 and its last 64-column
+    strip (every row tile)."""
     import shlo_hip
     from shlo_hip import configs
     B, N, K, M = 16, 1024, 4096, 4096
     a = shlo_hip.fill_random((B, N, K), 31, 1, 1.0)
     b = shlo_hip.fill_random((B, K, M), 32, 1, 1.0)
     y = shlo_hip.Module(configs.dot_module(N, K, M, B)).prepare(0, True).call([a, b])[0]
-    for bi, rows in ((0, (0, 777)), (11, (1023, 64))):
-        bs = shlo_hip.slice_(b, (bi, 0, 0), (bi + 1, K, M), (1, 1, 1)).numpy()[0]
-        for n in rows:
-            arow = shlo_hip.slice_(a, (bi, n, 0), (bi + 1, n + 1, K), (1, 1, 1)).numpy()[0]
-            want = oracle.dot_general_bnk(arow[None], np.ascontiguousarray(bs.T)[None])[0]
-            got = shlo_hip.slice_(y, (bi, n, 0), (bi + 1, n + 1, M), (1, 1, 1)).numpy()[0]
-            assert same_bits(got, want), (bi, n)
+
+    def sl(arr, start, stop):
+        return shlo_hip.slice_(arr, start, stop, (1, 1, 1)).numpy()[0]
+
+    for bi, n0 in ((0, 0), (11, 0), (15, N - 64)):
+        bt = np.ascontiguousarray(sl(b, (bi, 0, 0), (bi + 1, K, M)).T)  # [M, K]
+        arows = sl(a, (bi, n0, 0), (bi + 1, n0 + 64, K))
+        want = oracle.dot_general_bnk(arows[None], bt[None])[0]
+        assert same_bits(sl(y, (bi, n0, 0), (bi + 1, n0 + 64, M)), want), (bi, n0)
+    bi = 15
+    bcols = np.ascontiguousarray(sl(b, (bi, 0, M - 64), (bi + 1, K, M)).T)  # [64, K]
+    want = oracle.dot_general_bnk(sl(a, (bi, 0, 0), (bi + 1, N, K))[None], bcols[None])[0]
+    assert same_bits(sl(y, (bi, 0, M - 64), (bi + 1, N, M)), want)
 
 
 @pytest.mark.parametrize("dims", [dict(layers=2, d=128, heads=2, ffn=256, frames=32, feats=263, batch=2),
@@ -106,10 +112,14 @@ def test_denoiser_vs_oracle(oracle, dims):
         assert not same_bits(got, want), fault
 
 
-def test_denoiser_config5_graph_equals_eager():
-    """The full config: 8 layers, d 512, 8 heads, FFN 2048, 256 frames x 263
-    features, batch 32; the compiled module repeated (--repeat) gives the same
-    bits every call, equal to the eager run."""
+def test_denoiser_config5_vs_oracle():
+    """The full config (8 layers, d 512, 8 heads, FFN 2048, 256 frames x 263
+    features, batch 32): the compiled module repeated (--repeat) gives the
+    same bits every call, equal to the eager run, and batch elements 0 and 31
+    equal the oracle's forward pass of that element alone (every op of the
+    module computes each output from one batch element, in an order that does
+    not depend on the batch size)."""
+    import denoiser_ref
     import shlo_hip
     from shlo_hip import configs
     D = configs.Denoiser()
@@ -123,3 +133,10 @@ def test_denoiser_config5_graph_equals_eager():
                                                       shlo_hip.view(e, shlo_hip.U32))) == 0
     y = e.numpy()
     assert y.shape == (32, 256, 263) and np.all(np.isfinite(y))
+    host = denoiser_ref.host_args(D)
+    names = [nm for nm, _, _ in D.args()]
+    D1 = configs.Denoiser(batch=1)
+    for bi in (0, 31):
+        one = [h[bi:bi + 1] if nm in ("x", "temb") else h for nm, h in zip(names, host)]
+        want = denoiser_ref.forward(D1, one)
+        assert same_bits(y[bi:bi + 1], want), bi
