@@ -524,6 +524,10 @@ int shlo_device_info(char *name, size_t cap, int *cus, uint64_t *pool_bytes) {
   });
 }
 
+int shlo_count_nonzero_noalloc(const void *data, uint64_t count, uint32_t elem_bytes, uint64_t *out_device) {
+  return guard("count_nonzero_noalloc", [&] { shlo::count_nonzero_noalloc(data, count, elem_bytes, out_device); });
+}
+
 int shlo_last_dot_kernel(char *name, size_t cap) {
   return guard("last_dot_kernel", [&] {
     need(name, "name");

@@ -130,6 +130,11 @@ float erff_host(float x);
 // row tails (no reference counterpart: the exhaustive check of that expf).
 ArrayP expf_map(uint32_t base, uint32_t count);
 float expf_host(float x);
+// count_nonzero over `count` elements of elem_bytes (1, 2, 4, 8) at device
+// address `data`, written to the device word `out`, queued on the executor's
+// stream; its partial counts live in a static device array, so it allocates
+// nothing (noalloc.hip).
+void count_nonzero_noalloc(const void *data, uint64_t count, uint32_t elem_bytes, uint64_t *out);
 // Refuses a row tail (cols % 4 != 0) unless the pinned flavour is selected.
 void require_tail_expf(const char *op, int64_t cols);
 

@@ -237,6 +237,18 @@ int shlo_timer_stop(float *ms);
 int shlo_time_apply(shlo_fn *f, const shlo_arr *const *inputs, size_t nin, int reps, float *ms);
 /* Device name, compute units and the bytes the array pool holds. */
 int shlo_device_info(char *name, size_t cap, int *cus, uint64_t *pool_bytes);
+/* No counterpart in the reference.  shlo_count_nonzero for callers that
+ * cannot allocate device memory (code under HIP graph capture, tight serving
+ * loops, harnesses that forbid hipMalloc): counts the elements among `count`
+ * elements of elem_bytes (1, 2, 4 or 8) bytes at device address `data` whose
+ * bytes are not all zero, and writes the count to the device word
+ * `out_device`.  The work is queued on the executor's stream (shlo_sync
+ * waits for it).  Partial counts live in a static device array of 4096 words
+ * (32 KiB per GPU, held until the process ends), so the call allocates and
+ * frees nothing; at most 2^40 elements per call.  Both ranges must lie inside
+ * device allocations (checked; an error otherwise).  Calls that overlap on
+ * one GPU from different streams or processes race on the shared array. */
+int shlo_count_nonzero_noalloc(const void *data, uint64_t count, uint32_t elem_bytes, uint64_t *out_device);
 /* The kernel family and template arguments that the most recent dot_general
  * (or mul_mat) dispatch chose, e.g. "dot_mfma8d_k<RowVecB,ColQuadB,128,8>",
  * written NUL-terminated into name[cap] ("" before the first dispatch).  Lets
