@@ -71,9 +71,12 @@ void orc_mul_mat(const float *w, const float *x, float *y, int64_t K, int64_t M,
 float orc_ggml_v_expf(float x);
 
 /* Correctly rounded binary32 exp and erf (what the pinned ggml build links,
- * CORE-MATH expf/erff, ref/build.sh:52).  Evaluated as libquadmath expq/erfq
- * at 113 bits and rounded once.  Pinned against MPFR (tests/golden and the
- * exhaustive check script) and by gelu_erf_* / *_tail hashes. */
+ * CORE-MATH expf/erff, ref/build.sh:52).  expf: libquadmath expq at 113 bits,
+ * rounded once.  erff: glibc's binary64 erf rounded to binary32 where that
+ * rounding is provably the correct one, else erfq at 113 bits (see
+ * oracle.c).  Pinned against MPFR on all 2^32 inputs (the chunk checksums in
+ * tests/golden, checked by tests/test_oracle_erff.py) and by the gelu_erf_* /
+ * *_tail hashes. */
 float orc_expf_cr(float x);
 float orc_erff_cr(float x);
 
