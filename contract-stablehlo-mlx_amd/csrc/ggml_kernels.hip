@@ -1165,6 +1165,239 @@ __global__ void __launch_bounds__(256) soft_max_tail_k(int64_t rows, int cols, f
   if (lane < T) y[4 * G + lane] = et * inv;
 }
 
+// ---- rows longer than 4096 columns -------------------------------------------------
+//
+// A row that does not fit one wave's registers is streamed: each lane takes
+// the four-element groups g = lane + 64 j (j = 0 .. J - 1, J = ceil(G / 64))
+// in passes over global memory.  The in-order binary64 sums are decided as
+// in ordered_sum_apply, with the interval re-derived for n terms: the
+// in-order chain S lies within (n - 1) 2^-53 of the exact total and the tree
+// sum T (a lane's serial sum of J parts and one tail value, then six
+// butterfly levels) within (J + 7) 2^-53, so S lies in T (1 -+ delta) with
+// delta = (n + J + 8) 2^-52, twice their sum; f(T (1 - delta)) == f(T (1 +
+// delta)) fixes f(S).  The exactness test holds unchanged: T falls short of
+// the exact total by a relative (J + 7) 2^-53 < 2^-20 for any row below 2^31
+// columns.  The walk takes the parts again, in group order, from `part_at`.
+template <class PartAt, class Fin>
+__device__ float ordered_sum_long(double ls, int le, int G, float tail, int T, PartAt part_at, Fin fin) {
+  const int lane = threadIdx.x % kWave;
+  if (lane < T) {
+    ls = ls + (double)tail;
+    le = min(le, part_ulp_exp(tail));
+  }
+  ls = wave_sum_d(ls);
+  le = wave_min_i(le);
+  if (ls <= exact_limit(le)) return fin(ls);
+  const int J = (G + kWave - 1) / kWave;
+  const double d = ls * ((double)(G + T + J + 8) * 0x1p-52);
+  const float f_lo = fin(ls - d), f_hi = fin(ls + d);
+  if (f_lo == f_hi) return f_lo;  // false for NaN and infinity
+  double s = 0.0;
+  for (int j = 0; j < J; j++) {
+    const int g = kWave * j + lane;
+    const float p = g < G ? part_at(g) : 0.0f;
+    const double seg = row16_sum((double)p);
+    const int sege = row16_min(part_ulp_exp(p));
+#pragma unroll
+    for (int r = 0; r < 4; r++) {
+      if (kWave * j + 16 * r >= G) break;
+      const double t = s + lane_d(seg, 16 * r);
+      const double lim_p = exact_limit(__builtin_amdgcn_readlane(sege, 16 * r));
+      const uint32_t hs = (uint32_t)(__builtin_bit_cast(uint64_t, s) >> 32);
+      const double lim_s = __builtin_bit_cast(double, (uint64_t)((hs & 0xFFF00000u) | 0x000FFFFEu) << 32);
+      if (t <= lim_p && (s == 0.0 || t <= lim_s)) {
+        s = t;
+      } else {
+        const int n = min(16, G - (kWave * j + 16 * r));
+#pragma unroll 1
+        for (int i = 0; i < n; i++) s = s + (double)lane_f(p, 16 * r + i);
+      }
+    }
+  }
+  for (int l = 0; l < T; l++) s = s + (double)lane_f(tail, l);
+  return fin(s);
+}
+
+// Group g of a row (four elements from p + 4 g): a float4 load when rows are
+// 16-byte aligned (cols % 4 == 0), else four scalar loads.
+template <bool ALIGNED>
+__device__ __forceinline__ float4 row_group(const float *p, int g) {
+  if (ALIGNED) return ld4(p + 4 * (int64_t)g);
+  const float *q = p + 4 * (int64_t)g;
+  return make_float4(q[0], q[1], q[2], q[3]);
+}
+template <bool ALIGNED>
+__device__ __forceinline__ void row_group_st(float *p, int g, float4 v) {
+  if (ALIGNED) {
+    st4(p + 4 * (int64_t)g, v);
+    return;
+  }
+  float *q = p + 4 * (int64_t)g;
+  q[0] = v.x, q[1] = v.y, q[2] = v.z, q[3] = v.w;
+}
+
+// ggml soft_max on rows of any length (Shaders.lean:100-123), one wave per
+// row: pass 1 the maximum of x*sc; pass 2 e = ggml_v_expf(x*sc - mx) stored
+// to y (as ggml does) with each group's vaddvq_f32 part summed per lane, the
+// row tail (pinned flavour) through the correctly rounded expf; the
+// denominator decided by ordered_sum_long, whose walk re-reads e from y (each
+// lane reads back only the groups it wrote); pass 3 y *= inv.
+template <bool ALIGNED>
+__global__ void __launch_bounds__(256) soft_max_long_k(int64_t rows, int cols, float sc, int float_sum,
+                                                       const float *__restrict__ X, float *__restrict__ Y) {
+  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  const int G = cols / 4, T = cols % 4;
+  const int64_t row = blockIdx.x * 4LL + wave;
+  if (row >= rows) return;  // the whole wave; no barrier follows
+  const float *x = X + row * cols;
+  float *y = Y + row * cols;
+  float mx = -__builtin_inff();
+  for (int g = lane; g < G; g += kWave) {
+    const float4 v = row_group<ALIGNED>(x, g);
+    mx = __builtin_fmaxf(mx, __builtin_fmaxf(__builtin_fmaxf(v.x * sc, v.y * sc),
+                                             __builtin_fmaxf(v.z * sc, v.w * sc)));
+  }
+  if (lane < T) mx = __builtin_fmaxf(mx, x[4 * G + lane] * sc);
+  mx = wave_max_f(mx);
+  double ls = 0.0;
+  int le = 255;
+  auto part_of = [](float4 e) { return (e.x + e.y) + (e.z + e.w); };
+  for (int g = lane; g < G; g += kWave) {
+    const float4 v = row_group<ALIGNED>(x, g);
+    const float4 e = make_float4(ggml_v_expf(v.x * sc - mx), ggml_v_expf(v.y * sc - mx),
+                                 ggml_v_expf(v.z * sc - mx), ggml_v_expf(v.w * sc - mx));
+    row_group_st<ALIGNED>(y, g, e);
+    const float p = part_of(e);
+    ls = ls + (double)p;
+    le = min(le, part_ulp_exp(p));
+  }
+  float et = 0.0f;
+  if (lane < T) {
+    et = expfk::expf_cr(x[4 * G + lane] * sc - mx);
+    y[4 * G + lane] = et;
+  }
+  auto part_at = [&](int g) { return part_of(row_group<ALIGNED>(y, g)); };
+  float inv;
+  if (float_sum) {  // planted: the denominator summed in binary32 in group order (Shaders.lean:120-122)
+    float fs = 0.0f;
+    const int J = (G + kWave - 1) / kWave;
+    for (int j = 0; j < J; j++) {
+      const int g = kWave * j + lane;
+      const float p = g < G ? part_at(g) : 0.0f;
+      const int n = min(kWave, G - kWave * j);
+      for (int l = 0; l < n; l++) fs = fs + lane_f(p, l);
+    }
+    for (int l = 0; l < T; l++) fs = fs + lane_f(et, l);
+    inv = 1.0f / fs;
+  } else {
+    inv = ordered_sum_long(ls, le, G, et, T, part_at, [](double v) { return (float)(1.0 / v); });
+  }
+  for (int g = lane; g < G; g += kWave) {
+    const float4 e = row_group<ALIGNED>(y, g);
+    row_group_st<ALIGNED>(y, g, make_float4(e.x * inv, e.y * inv, e.z * inv, e.w * inv));
+  }
+  if (lane < T) y[4 * G + lane] = et * inv;
+}
+
+// ggml norm on rows of any length (Shaders.lean:130-166), one wave per row:
+// pass 1 the mean's binary64 sum (decided as in norm_rows_k, the walk
+// re-reading x 64 elements at a time); pass 2 the variance's group parts of
+// q = (x - mean)^2, decided by ordered_sum_long (the walk recomputes them
+// from x); pass 3 y = (x - mean) * scale.
+template <bool ALIGNED>
+__global__ void __launch_bounds__(256) norm_long_k(int64_t rows, int cols, float eps, const float *__restrict__ X,
+                                                   float *__restrict__ Y) {
+  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  const int G = cols / 4, T = cols - 4 * G;
+  const int J = (G + kWave - 1) / kWave;
+  const int64_t row = blockIdx.x * 4LL + wave;
+  if (row >= rows) return;  // the whole wave; no barrier follows
+  const float *x = X + row * cols;
+  float *y = Y + row * cols;
+  double ls = 0.0, la = 0.0;
+  int le = 255;
+  auto take = [&](float v) {
+    ls = ls + (double)v;
+    la = la + (double)__builtin_fabsf(v);
+    le = min(le, part_ulp_exp(v));
+  };
+  for (int g = lane; g < G; g += kWave) {
+    const float4 v = row_group<ALIGNED>(x, g);
+    take(v.x);
+    take(v.y);
+    take(v.z);
+    take(v.w);
+  }
+  const float et = lane < T ? x[4 * G + lane] : 0.0f;
+  take(et);
+  ls = wave_sum_d(ls);
+  la = wave_sum_d(la);
+  le = wave_min_i(le);
+  const float fc = (float)cols;
+  float mean;
+  if (la <= exact_limit(le)) {
+    mean = (float)ls / fc;
+  } else {
+    const double d = la * ((double)(cols + 4 * J + 8) * 0x1p-52);
+    const float lo = (float)(ls - d) / fc, hi = (float)(ls + d) / fc;
+    if (lo == hi) {  // false for NaN
+      mean = lo;
+    } else {
+      double s = 0.0;
+      for (int j = 0; j < J; j++) {
+        const int g = kWave * j + lane;
+        const float4 q = g < G ? row_group<ALIGNED>(x, g) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+        const double seg = row16_sum(((double)q.x + (double)q.y) + ((double)q.z + (double)q.w));
+        const double sega = row16_sum(((double)__builtin_fabsf(q.x) + (double)__builtin_fabsf(q.y)) +
+                                      ((double)__builtin_fabsf(q.z) + (double)__builtin_fabsf(q.w)));
+        const int sege = row16_min(min(min(part_ulp_exp(q.x), part_ulp_exp(q.y)),
+                                       min(part_ulp_exp(q.z), part_ulp_exp(q.w))));
+#pragma unroll
+        for (int r = 0; r < 4; r++) {
+          if (kWave * j + 16 * r >= G) break;
+          const int e_min = min(__builtin_amdgcn_readlane(sege, 16 * r), low_bit_exp(s));
+          if (__builtin_fabs(s) + lane_d(sega, 16 * r) <= exact_limit(e_min)) {
+            s = s + lane_d(seg, 16 * r);
+          } else {
+            const int n = min(16, G - (kWave * j + 16 * r));
+#pragma unroll 1
+            for (int i = 16 * r; i < 16 * r + n; i++) {
+              s = s + (double)lane_f(q.x, i);
+              s = s + (double)lane_f(q.y, i);
+              s = s + (double)lane_f(q.z, i);
+              s = s + (double)lane_f(q.w, i);
+            }
+          }
+        }
+      }
+      for (int l = 0; l < T; l++) s = s + (double)lane_f(et, l);
+      mean = (float)s / fc;
+    }
+  }
+  auto part_at = [&](int g) {
+    const float4 v = row_group<ALIGNED>(x, g);
+    const float d0 = v.x - mean, d1 = v.y - mean, d2 = v.z - mean, d3 = v.w - mean;
+    return (d0 * d0 + d1 * d1) + (d2 * d2 + d3 * d3);
+  };
+  double vs = 0.0;
+  int ve = 255;
+  for (int g = lane; g < G; g += kWave) {
+    const float p = part_at(g);
+    vs = vs + (double)p;
+    ve = min(ve, part_ulp_exp(p));
+  }
+  const float dt = et - mean, qt = dt * dt;
+  const double dc = (double)cols;
+  const float var = ordered_sum_long(vs, ve, G, qt, T, part_at, [dc](double v) { return (float)(v / dc); });
+  const float scl = 1.0f / sqrtf(var + eps);
+  for (int g = lane; g < G; g += kWave) {
+    const float4 v = row_group<ALIGNED>(x, g);
+    row_group_st<ALIGNED>(y, g, make_float4((v.x - mean) * scl, (v.y - mean) * scl, (v.z - mean) * scl,
+                                            (v.w - mean) * scl));
+  }
+  if (lane < T) y[4 * G + lane] = dt * scl;
+}
+
 int env_int(const char *name, int dflt) {
   const char *s = getenv(name);
   return s ? atoi(s) : dflt;
@@ -1172,20 +1405,17 @@ int env_int(const char *name, int dflt) {
 
 // ---- norm ---------------------------------------------------------------------------
 
-// The planted norm (Shaders.lean:147-166 with binary32 sums and the GPU's own
-// approximate reciprocal and square root): one wave per row, the row staged in
-// LDS, the sequential sums on lane 0.
+// The planted norm (Shaders.lean:137-146: binary32 sums and the GPU's own
+// approximate reciprocal and square root): one wave per row, the sequential
+// sums on lane 0 reading the row from global memory (rows of any length).
 __global__ void __launch_bounds__(256) norm_planted_k(int64_t rows, int cols, float eps,
                                                       const float *__restrict__ X, float *__restrict__ Y) {
-  extern __shared__ float lds[];
   const int waves = blockDim.x / kWave;
   const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
-  float *xr = lds + wave * (cols + 4);
   for (int64_t row = blockIdx.x * (int64_t)waves + wave; row < rows; row += (int64_t)gridDim.x * waves) {
     const float *x = X + row * cols;
+    const float *xr = x;
     float *y = Y + row * cols;
-    for (int i = lane; i < cols; i += kWave) xr[i] = x[i];
-    wave_sync();
     float mean = 0.0f, scl = 0.0f;
     if (lane == 0) {
       float s = 0.0f;
@@ -1201,7 +1431,6 @@ __global__ void __launch_bounds__(256) norm_planted_k(int64_t rows, int cols, fl
     mean = __shfl(mean, 0, kWave);
     scl = __shfl(scl, 0, kWave);
     for (int i = lane; i < cols; i += kWave) y[i] = (xr[i] - mean) * scl;
-    wave_sync();
   }
 }
 
@@ -1710,6 +1939,16 @@ ArrayP mul_mat(const ArrayP &w0, const ArrayP &x0, int64_t K, int64_t M, int64_t
   return dot_ggml(DotOperand{x, N * K, K, 1}, DotOperand{w, wbs, K, 1}, B, N, M, K, tail);
 }
 
+// The row kernels load four-element groups as 16-byte loads from the start
+// of the array: a contiguous view at an offset that is not a multiple of 16
+// bytes is first copied to a fresh (256-byte aligned) block.
+ArrayP aligned_rows(const ArrayP &x) {
+  if (!x->buf || (uintptr_t)x->data() % 16 == 0) return x;
+  auto c = new_array(x->dtype, x->shape);
+  copy_into(c, x);
+  return c;
+}
+
 // A row tail (cols % 4 elements) goes through ggml-cpu's scalar expf: the
 // pinned flavour's is correctly rounded and carried; the stock flavour's is
 // Apple libsystem_m's, closed code, and refused as the reference refuses it
@@ -1725,11 +1964,26 @@ ArrayP soft_max(const ArrayP &x0, int64_t rows, int64_t cols, uint32_t scale_bit
   if (x0->dtype != kF32) fail("ggml.soft_max: f32 only");
   if (rows * cols != x0->size()) fail("ggml.soft_max: rows*cols is not the element count");
   require_tail_expf("ggml.soft_max", cols);
-  if (cols > 4 * kWave * 16) fail("ggml.soft_max: rows above 4096 columns are not carried");
-  ArrayP x = contiguous(x0);
+  if (cols > 0x7FFFFFFF) fail("ggml.soft_max: rows of 2^31 columns or more are not carried");
+  ArrayP x = aligned_rows(contiguous(x0));
   auto y = new_array(kF32, x->shape);
   if (rows == 0 || cols == 0) return y;
   const float sc = bits_f(scale_bits);
+  if (cols > 4 * kWave * 16) {  // rows that do not fit one wave's registers
+    const int64_t nblk = (rows + 3) / 4;
+    if (nblk > 0x7FFFFFFF) fail("ggml.soft_max: too many rows");
+    const unsigned grid = (unsigned)nblk;
+    const float *px = (const float *)x->data();
+    float *py = (float *)y->data();
+    const int c = (int)cols, fs = float_sum ? 1 : 0;
+    ArrayP kx = x;
+    launch([=](hipStream_t s) {
+      (void)kx;
+      if (c % 4) soft_max_long_k<false><<<grid, 256, 0, s>>>(rows, c, sc, fs, px, py);
+      else soft_max_long_k<true><<<grid, 256, 0, s>>>(rows, c, sc, fs, px, py);
+    });
+    return y;
+  }
   if (cols % 4) {
     const int G = (int)(cols / 4);
     const int Jt = std::max(1, (G + kWave - 1) / kWave);
@@ -1787,11 +2041,11 @@ ArrayP norm(const ArrayP &x0, int64_t rows, int64_t cols, uint32_t eps_bits, boo
             const std::vector<FusedOp> &epi) {
   if (x0->dtype != kF32) fail("ggml.norm: f32 only");
   if (rows * cols != x0->size()) fail("ggml.norm: rows*cols is not the element count");
-  if (cols > 4096) fail("ggml.norm: rows above 4096 columns are not carried");
+  if (cols > 0x7FFFFFFF) fail("ggml.norm: rows of 2^31 columns or more are not carried");
   if (gpu_ops && !epi.empty()) fail("ggml.norm: no fused ops with the planted binary32 sums");
   for (const FusedOp &o : epi)
     if (o.code == kEpiGeluErf) fail("ggml.norm: gelu_erf is not a fused op of norm");
-  ArrayP x = contiguous(x0);
+  ArrayP x = aligned_rows(contiguous(x0));
   auto y = new_array(kF32, x->shape);
   if (rows == 0 || cols == 0) return y;
   const float *px = (const float *)x->data();
@@ -1800,19 +2054,27 @@ ArrayP norm(const ArrayP &x0, int64_t rows, int64_t cols, uint32_t eps_bits, boo
   const int c = (int)cols;
   ArrayP kx = x;
   if (gpu_ops) {  // planted: binary32 sums and the GPU's own / and sqrt
-    // LDS per wave: the row; at most 64 KiB per block.
-    const int per_wave = (int)(cols + 4) * (int)sizeof(float);
-    const int waves = std::max(1, std::min(4, 65536 / per_wave));
-    const int lds = waves * per_wave;
-    const unsigned grid = grid_cap(rows, waves, 1 << 20);
+    const unsigned grid = grid_cap(rows, 4, 1 << 20);
     launch([=](hipStream_t s) {
       (void)kx;
-      norm_planted_k<<<grid, kWave * waves, lds, s>>>(rows, c, eps, px, py);
+      norm_planted_k<<<grid, kWave * 4, 0, s>>>(rows, c, eps, px, py);
     });
     return y;
   }
   std::vector<ArrayP> ek;
   const Epilogue ep = make_epilogue(epi, &ek);
+  if (cols > 4096) {  // rows that do not fit one wave's registers
+    if (ep.n > 0) fail("ggml.norm: fused ops need rows of at most 1024 columns");
+    const int64_t nblk = (rows + 3) / 4;
+    if (nblk > 0x7FFFFFFF) fail("ggml.norm: too many rows");
+    const unsigned grid = (unsigned)nblk;
+    launch([=](hipStream_t s) {
+      (void)kx;
+      if (c % 4) norm_long_k<false><<<grid, 256, 0, s>>>(rows, c, eps, px, py);
+      else norm_long_k<true><<<grid, 256, 0, s>>>(rows, c, eps, px, py);
+    });
+    return y;
+  }
   const int J = std::max<int>(1, (int)((cols / 4 + kWave - 1) / kWave));
   if (ep.n > 0 && J > kNormEpiJ) fail("ggml.norm: fused ops need rows of at most 1024 columns");
   const bool full = cols == 4LL * kWave * J, fused = ep.n > 0;
