@@ -658,9 +658,9 @@ __device__ __forceinline__ void xcd_tile(uint32_t &tx, uint32_t &ty) {
   ty = id / gx;
 }
 
-template <int LX, int LW, int KC, int WAVES>
+template <int LX, int LW, int KC, int WAVES, bool EDGE>
 __global__ void __launch_bounds__(WAVES * 64, 2) dot_mfma8d_k(MfmaOperand X, MfmaOperand W, int64_t N, int64_t M,
-                                                           int64_t K, int tiles_m, Epilogue ep,
+                                                           int64_t K, int tail, int tiles_m, Epilogue ep,
                                                            float *__restrict__ Y) {
   static_assert(LX == kLoadRowVecB && (LW == kLoadColQuadB || LW == kLoadRowVecB), "direct loads: lhs along k");
   static_assert(KC == 128 || KC == 64, "stages of 128 or 64 k");
@@ -693,7 +693,12 @@ __global__ void __launch_bounds__(WAVES * 64, 2) dot_mfma8d_k(MfmaOperand X, Mfm
   if (WAVES == 4 && gridDim.y > 1) xcd_tile(tx, ty);
   const int64_t b = ty;
   const int64_t n0 = (int64_t)(tx / tiles_m) * TN, m0 = (int64_t)(tx % tiles_m) * kMT;
-  const int nst = (int)(K / KC);  // every stage full (the host checks)
+  // The stages cover the blocks of 16 (np = K & ~15, a whole number of
+  // stages: the host checks).  Every row a tile loads exists (rows padded to
+  // the tile: the host checks).  EDGE: a serial tail (np < K) and outputs
+  // past N or M (not stored); without it, np == K and every tile is whole.
+  const int64_t np = EDGE ? K & ~(int64_t)15 : K;
+  const int nst = (int)(np / KC);
 
   const int64_t nl = n0 + wn * 32 + 4 * (lane >> 5) + 16 * rh, ml = m0 + wm * 32 + (lane & 31);
   auto orow = [&](int r) { return nl + 8 * (r / 4) + r % 4; };
@@ -810,6 +815,26 @@ __global__ void __launch_bounds__(WAVES * 64, 2) dot_mfma8d_k(MfmaOperand X, Mfm
 #pragma unroll
     for (int q = 0; q < 4; q++) give[(r * 4 + q) * 64 + lane] = rh ? t4[r][q] : t4[8 + r][q];
   __syncthreads();
+  // EDGE with a tail: the tile's tail operands (lhs rows n0.., rhs rows m0..,
+  // k in [np, K)) go to LDS once, in the buffers the exchange leaves free
+  // (rows past N or M read row N - 1 or M - 1; those outputs are discarded).
+  const int tl = (int)(K - np);
+  float *tlx = reinterpret_cast<float *>(WAVES == 8 ? dw0 : dx0), *tlw = tlx + TN * 16;
+  static_assert((TN + kMT) * 16 <= 4 * (WAVES == 8 ? WCH : XCH), "the tail operands fit their buffer");
+  if (EDGE && tl > 0) {
+    const float *xb = X.p + boff(X, b), *wb = W.p + boff(W, b);
+    for (int i = threadIdx.x; i < (TN + kMT) * tl; i += WAVES * 64) {
+      const int r = i / tl, k = i - r * tl;
+      if (r < TN) {
+        const int64_t row = n0 + r < N ? n0 + r : N - 1;
+        tlx[r * 16 + k] = xb[row * X.sf + (np + k) * X.sk];
+      } else {
+        const int64_t row = m0 + (r - TN) < M ? m0 + (r - TN) : M - 1;
+        tlw[(r - TN) * 16 + k] = wb[row * W.sf + (np + k) * W.sk];
+      }
+    }
+  }
+  if (EDGE) __syncthreads();
   float out[8];
 #pragma unroll
   for (int r = 0; r < 8; r++) {
@@ -821,7 +846,30 @@ __global__ void __launch_bounds__(WAVES * 64, 2) dot_mfma8d_k(MfmaOperand X, Mfm
     }
     out[r] = (w[0] + w[1]) + (w[2] + w[3]);  // vaddvq_f32
   }
-  dot_store8<true, NE>(X, W, b, N, M, K, K, kTailStock, true, out, ep, pre, gt, Y, orow, ocol);
+  if (EDGE && tl > 0) {  // the serial tail of dot_finish, operands from LDS
+    const float *wt = tlw + (ocol(0) - m0) * 16;
+#pragma unroll
+    for (int r = 0; r < 8; r++) {
+      const float *xt = tlx + (orow(r) - n0) * 16;
+      float sumf = out[r];
+      if (tail == kTailPinned) {
+        for (int k = 0; k < tl; k++) {
+          const float p = wt[k] * xt[k];
+          sumf = sumf + p;
+        }
+      } else {
+        const int nq = tl >= 4 ? (tl & ~3) : 0;
+        for (int k = 0; k < nq; k++) {
+          const float p = wt[k] * xt[k];
+          sumf = sumf + p;
+        }
+        for (int k = nq; k < tl; k++) sumf = __builtin_fmaf(wt[k], xt[k], sumf);
+      }
+      out[r] = sumf;
+    }
+  }
+  const bool whole = !EDGE || (n0 + TN <= N && m0 + kMT <= M);
+  dot_store8<true, NE>(X, W, b, N, M, K, K, tail, whole, out, ep, pre, gt, Y, orow, ocol);
 }
 
 
@@ -1761,6 +1809,27 @@ Epilogue make_epilogue(const std::vector<FusedOp> &ops, std::vector<ArrayP> *kee
   return ep;
 }
 
+// A copy of a dot operand (element (b, r, k) for b < B, r < rows, k < K) in a
+// layout the direct kernel reads: [B][R][Kp] (along k, rows Kp = K rounded up
+// to 4 floats apart) or [B][K][R] (rows contiguous), R = rows rounded up to
+// the tile.  Padding never reaches a stored output: padded rows feed only
+// outputs past N or M, which are not stored, and k past K is never read.
+DotOperand padded_operand(const DotOperand &d, int64_t B, int64_t rows, int64_t K, bool along_k) {
+  const int64_t R = (rows + kMT - 1) / kMT * kMT, Kp = (K + 3) / 4 * 4;
+  auto p = new_array(kF32, along_k ? Shape{B, R, Kp} : Shape{B, K, R});
+  auto src = std::make_shared<Array>();
+  src->buf = d.arr->buf;
+  src->offset = d.arr->offset;
+  src->dtype = kF32;
+  src->shape = Shape{B / d.nb2, d.nb2, rows, K};
+  src->strides = Shape{d.sb, d.sb2, d.sf, d.sk};
+  copy_to_strides(src, along_k ? Shape{d.nb2 * R * Kp, R * Kp, Kp, 1} : Shape{d.nb2 * K * R, K * R, 1, R},
+                  p->data());
+  DotOperand o{p, along_k ? R * Kp : K * R, along_k ? Kp : 1, along_k ? 1 : R, 0, 1};
+  o.rows_alloc = R;
+  return o;
+}
+
 ArrayP dot_ggml(const DotOperand &lhs, const DotOperand &rhs, int64_t B, int64_t N, int64_t M, int64_t K, int tail,
                 const std::vector<FusedOp> &epi) {
   if (lhs.arr->dtype != kF32 || rhs.arr->dtype != kF32) fail("dot_general: f32 operands only");
@@ -1787,7 +1856,9 @@ ArrayP dot_ggml(const DotOperand &lhs, const DotOperand &rhs, int64_t B, int64_t
       if (sf == 1) return (int)kLoadColVec;
       return (int)kLoadScalar;
     };
-    int lx = loader(L, lb, ln, lk, N, lhs), lw = loader(R, rb, rm, rk, M, rhs);
+    // Rows readable per batch: a padded copy's, else the logical rows.
+    const int64_t Nr = lhs.rows_alloc ? lhs.rows_alloc : N, Mr = rhs.rows_alloc ? rhs.rows_alloc : M;
+    int lx = loader(L, lb, ln, lk, Nr, lhs), lw = loader(R, rb, rm, rk, Mr, rhs);
     // The buffer loaders need every read in range by construction: rows a
     // multiple of the tile, every stage full, non-negative strides, and the
     // largest byte offset within a batch below 2^31.
@@ -1800,8 +1871,8 @@ ArrayP dot_ggml(const DotOperand &lhs, const DotOperand &rhs, int64_t B, int64_t
     auto buf_ok = [&](int64_t sf, int64_t sk, int64_t sb, int64_t rows) {
       return full_stages && in_range(sf, sk, sb, rows);
     };
-    if (((lx == kLoadRowVec && ln % 4 == 0) || lx == kLoadColQuad) && buf_ok(ln, lk, lb, N) &&
-        ((lw == kLoadRowVec && rm % 4 == 0) || lw == kLoadColQuad) && buf_ok(rm, rk, rb, M)) {
+    if (((lx == kLoadRowVec && ln % 4 == 0) || lx == kLoadColQuad) && buf_ok(ln, lk, lb, Nr) &&
+        ((lw == kLoadRowVec && rm % 4 == 0) || lw == kLoadColQuad) && buf_ok(rm, rk, rb, Mr)) {
       lx = lx == kLoadRowVec ? (int)kLoadRowVecB : (int)kLoadColQuadB;
       lw = lw == kLoadRowVec ? (int)kLoadRowVecB : (int)kLoadColQuadB;
     }
@@ -1834,17 +1905,30 @@ ArrayP dot_ggml(const DotOperand &lhs, const DotOperand &rhs, int64_t B, int64_t
     // K = 256 and 512 products 6.11 against 5.57 ms, its [8192,512] x
     // [512,263] output projection 64 against 57 us, config 3 5.44 against
     // 5.16 ms).
-    // The direct kernel has no serial tail: it needs K a whole number of
-    // stages (the buffer loaders alone only need whole stages of blocks).
+    // The direct kernel's stages cover the blocks of 16 (np = K & ~15, a
+    // whole number of stages); the serial tail runs in its store.
+    const int64_t np = K & ~(int64_t)15;
     int dkc = 0;
-    if (lx == kLoadRowVecB && (lw == kLoadColQuadB || lw == kLoadRowVecB) && K % kKC == 0) {
+    if (lx == kLoadRowVecB && (lw == kLoadColQuadB || lw == kLoadRowVecB)) {
       dkc = kKC;
-    } else if (lx == kLoadRowVec && lw == kLoadRowVec && K % 64 == 0 && K >= 64 && ln % 4 == 0 && rm % 4 == 0 &&
-               in_range(ln, lk, lb, N) && in_range(rm, rk, rb, M)) {
+    } else if (lx == kLoadRowVec && lw == kLoadRowVec && np % 64 == 0 && np >= 64 && ln % 4 == 0 && rm % 4 == 0 &&
+               in_range(ln, lk, lb, Nr) && in_range(rm, rk, rb, Mr)) {
       dkc = 64;
       lx = lw = kLoadRowVecB;
     }
     const bool direct = dkc > 0;
+    // A large product with an lhs along k and an rhs along its free dim or
+    // along k that cannot go direct in place (rows not 16-byte aligned, row
+    // counts not multiples of the tile, e.g. the denoiser's 263-wide
+    // projections) runs on padded copies: one pass over each operand buys the
+    // direct kernel.
+    if (!direct && lhs.rows_alloc == 0 && rhs.rows_alloc == 0 && lk == 1 && (rm == 1 || rk == 1) &&
+        np >= kKC && np % kKC == 0 && (double)B * (double)N * (double)M * (double)np >= (double)(1 << 27) &&
+        ((double)std::max(N, M) + kMT) * ((double)K + 4) * 4.0 < (double)(1LL << 31)) {
+      const DotOperand pl = padded_operand(lhs, B, N, K, true);
+      const DotOperand pr = padded_operand(rhs, B, M, K, rm != 1);
+      return dot_ggml(pl, pr, B, N, M, K, tail, epi);
+    }
     // The register-staged kernel is instantiated with the buffer loaders only
     // for a column-read lhs: a row-read lhs that did not go direct takes the
     // plain loaders (same elements, bounds-checked addressing).
@@ -1876,24 +1960,30 @@ ArrayP dot_ggml(const DotOperand &lhs, const DotOperand &rhs, int64_t B, int64_t
       g_last_dot = strf("dot_mfma8d_k<RowVecB,%s,%d,%d>", loader_name(lw), small ? 64 : dkc, small ? 4 : 8);
     else
       g_last_dot = strf("dot_mfma8_k<%s,%s>", loader_name(lx), loader_name(lw));
+    // Tiles that are not whole (rows past N or M, a tail) take the EDGE
+    // instances; the rest keep the leaner code (and three workgroups per CU).
+    const bool edge = np < K || N % (small ? 32 : kMT) != 0 || M % kMT != 0;
     launch([=](hipStream_t s) {
       (void)kl, (void)kr, (void)ek;
+#define DOT_D(lw_, kc_, waves_, grid_, th_, lds_)                                                              \
+  do {                                                                                                        \
+    if (edge)                                                                                                 \
+      dot_mfma8d_k<kLoadRowVecB, lw_, kc_, waves_, true><<<grid_, th_, lds_, s>>>(X, W, N, M, K, tl, tiles_m, ep, Y); \
+    else                                                                                                      \
+      dot_mfma8d_k<kLoadRowVecB, lw_, kc_, waves_, false><<<grid_, th_, lds_, s>>>(X, W, N, M, K, tl, tiles_m, ep, Y); \
+  } while (0)
       if (direct && small) {
-        if (lw == kLoadColQuadB)
-          dot_mfma8d_k<kLoadRowVecB, kLoadColQuadB, 64, 4><<<grid_s, 256, 0, s>>>(X, W, N, M, K, tiles_m, ep, Y);
-        else
-          dot_mfma8d_k<kLoadRowVecB, kLoadRowVecB, 64, 4><<<grid_s, 256, 0, s>>>(X, W, N, M, K, tiles_m, ep, Y);
+        if (lw == kLoadColQuadB) DOT_D(kLoadColQuadB, 64, 4, grid_s, 256, 0);
+        else DOT_D(kLoadRowVecB, 64, 4, grid_s, 256, 0);
         return;
       }
       if (direct) {
-        if (lw == kLoadColQuadB)
-          dot_mfma8d_k<kLoadRowVecB, kLoadColQuadB, kKC, 8><<<grid1, 512, glds, s>>>(X, W, N, M, K, tiles_m, ep, Y);
-        else if (dkc == kKC)
-          dot_mfma8d_k<kLoadRowVecB, kLoadRowVecB, kKC, 8><<<grid1, 512, glds, s>>>(X, W, N, M, K, tiles_m, ep, Y);
-        else
-          dot_mfma8d_k<kLoadRowVecB, kLoadRowVecB, 64, 8><<<grid1, 512, glds, s>>>(X, W, N, M, K, tiles_m, ep, Y);
+        if (lw == kLoadColQuadB) DOT_D(kLoadColQuadB, kKC, 8, grid1, 512, glds);
+        else if (dkc == kKC) DOT_D(kLoadRowVecB, kKC, 8, grid1, 512, glds);
+        else DOT_D(kLoadRowVecB, 64, 8, grid1, 512, glds);
         return;
       }
+#undef DOT_D
 #define DOT_CASE(a, c)                                                                    \
   if (lx == a && lw == c) {                                                               \
     dot_mfma8_k<a, c><<<grid1, 512, lds, s>>>(X, W, N, M, K, tl, tiles_m, ep, Y);         \

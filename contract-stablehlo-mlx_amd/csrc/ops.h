@@ -33,6 +33,9 @@ ArrayP empty_array();
 
 // ---- data movement and elementwise kernels ----------------------------------
 ArrayP contiguous(const ArrayP &a);
+// Copies src's elements (in its logical order) to dst_base laid out with
+// dst_strides (elements, one per dim of src), on the executor's stream.
+void copy_to_strides(const ArrayP &src, const Shape &dst_strides, char *dst_base);
 void copy_into(const std::shared_ptr<Array> &dst, const ArrayP &src);  // eager
 ArrayP concat(const std::vector<ArrayP> &xs, int axis);
 ArrayP astype(const ArrayP &a, uint8_t dtype);
@@ -73,6 +76,7 @@ struct DotOperand {
   ArrayP arr;       // keeps the buffer alive
   int64_t sb = 0, sf = 0, sk = 0;
   int64_t sb2 = 0, nb2 = 1;
+  int64_t rows_alloc = 0;  // rows readable in each batch (a padded copy's), 0: the logical rows
 };
 
 // One element-wise binary32 op fused into a producer's store: v = op(v, o)

@@ -617,6 +617,11 @@ void copy_strided(const ArrayP &src, const Shape &dst_strides, char *dst_base) {
 
 // ---- public ops -------------------------------------------------------------------
 
+void copy_to_strides(const ArrayP &src, const Shape &dst_strides, char *dst_base) {
+  if (dst_strides.size() != src->shape.size()) fail("copy: stride count does not match the rank");
+  copy_strided(src, dst_strides, dst_base);
+}
+
 ArrayP contiguous(const ArrayP &a) {
   if (a->contiguous()) return a;
   auto o = new_array(a->dtype, a->shape);

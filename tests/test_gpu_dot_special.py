@@ -193,10 +193,17 @@ CASES = [
     ("staged_rowvec_scalar", "nk", "strided", 2, 70, 44, 70, "dot_mfma8_k<RowVec,Scalar>"),
     ("staged_colquadB_rowvecB", "kn", "mk", 1, 64, 136, 64, "dot_mfma8_k<ColQuadB,RowVecB>"),
     ("staged_colquadB_colquadB", "kn", "km", 1, 64, 256, 128, "dot_mfma8_k<ColQuadB,ColQuadB>"),
-    # Rows multiples of 64 and whole stages of blocks, K not a whole number of
-    # stages: the direct kernel (which has no serial tail) must not take these.
-    ("buffer_rows_with_tail_colquad", "nk", "km", 1, 64, 132, 64, "dot_mfma8_k<RowVec,ColQuad>"),
-    ("buffer_rows_with_tail_rowvec", "nk", "mk", 1, 64, 140, 128, "dot_mfma8_k<RowVec,RowVec>"),
+    # Whole stages of blocks plus a tail (K % 16 != 0): the direct kernel runs
+    # the serial tail in its store.
+    ("direct_with_tail_colquad", "nk", "km", 1, 64, 132, 64, "dot_mfma8d_k<RowVecB,ColQuadB,64,4>"),
+    ("direct_with_tail_rowvec", "nk", "mk", 1, 64, 140, 128, "dot_mfma8d_k<RowVecB,RowVecB,64,4>"),
+    # Large products the direct kernel cannot read in place run on padded
+    # copies (rows 4-float aligned, row counts multiples of 64): an unaligned
+    # K = 263 lhs, a 263-wide rhs, edge tiles in both dims, a batch.
+    ("padded_lhs_k263", "nk", "km", 1, 1024, 263, 512, "dot_mfma8d_k<RowVecB,ColQuadB,64,4>"),
+    ("padded_rhs_m263", "nk", "km", 1, 1024, 512, 263, "dot_mfma8d_k<RowVecB,ColQuadB,64,4>"),
+    ("padded_edges_rowvec", "nk", "mk", 1, 210, 640, 1000, "dot_mfma8d_k<RowVecB,RowVecB,128,8>"),
+    ("padded_batched", "nk", "km", 3, 100, 270, 1800, "dot_mfma8d_k<RowVecB,ColQuadB,64,4>"),
     ("one_thread_per_output", "nk", "km", 65536, 1, 37, 2, "dot_ggml_simple<"),
 ]
 
