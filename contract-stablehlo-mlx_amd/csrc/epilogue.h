@@ -21,22 +21,20 @@ namespace shlo {
 // (StablehloMlx/Mlx.lean:88-108): maximum / minimum order -0 below +0
 // (mx::maximum).  A NaN operand propagates as on arm64 and x86 (the first
 // NaN operand, quieted, sign kept): the result is x + y, which the GPU's add
-// returns that way, where its subtract would flip a NaN's sign.
+// returns that way, where its subtract would flip a NaN's sign.  The NaN case
+// is a select, not a branch, so a wave never diverges over it.
 __host__ __device__ inline float f32_binary(uint32_t op, float x, float y) {
-  if (x != x || y != y) return x + y;
+  float r;
   switch (op) {
-    case kAdd: return x + y;
-    case kSub: return x - y;
-    case kMul: return x * y;
-    case kDiv: return x / y;  // correctly rounded: built with -fhip-fp32-correctly-rounded-divide-sqrt
-    case kMax:
-      if (x == y) return std::signbit(x) ? y : x;
-      return x > y ? x : y;
-    case kMin:
-      if (x == y) return std::signbit(x) ? x : y;
-      return x < y ? x : y;
-    default: return x;
+    case kAdd: r = x + y; break;
+    case kSub: r = x - y; break;
+    case kMul: r = x * y; break;
+    case kDiv: r = x / y; break;  // correctly rounded: built with -fhip-fp32-correctly-rounded-divide-sqrt
+    case kMax: r = x == y ? (std::signbit(x) ? y : x) : (x > y ? x : y); break;
+    case kMin: r = x == y ? (std::signbit(x) ? x : y) : (x < y ? x : y); break;
+    default: r = x; break;
   }
+  return __builtin_isunordered(x, y) ? x + y : r;
 }
 
 // Up to kMaxEpi ops applied in order to an output value v at index

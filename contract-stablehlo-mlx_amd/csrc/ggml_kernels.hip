@@ -1077,20 +1077,9 @@ __device__ __forceinline__ float softmax_inv(const float (&part)[J], int G, floa
 // FULL: every lane owns exactly J groups (cols == 256*J), so no group index
 // needs a bounds check.  UNIT: scale == 1, so x*sc is x (a NaN x makes the
 // whole row NaN either way, through its own part of the sum).
-template <int J, bool FULL, bool UNIT = false>
-__global__ void __launch_bounds__(256) soft_max_rows_k(int64_t rows, int cols, float sc, int float_sum,
-                                                       const float *__restrict__ X, float *__restrict__ Y) {
-  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
-  const int G = cols / 4;
-  const int64_t row = blockIdx.x * 4LL + wave;
-  if (row >= rows) return;  // the whole wave; no barrier follows
-  const float *x = X + row * cols;
-  float4 e[J];
-#pragma unroll
-  for (int j = 0; j < J; j++) {
-    const int g = lane + kWave * j;
-    if (FULL || g < G) e[j] = ld4_nt(x + 4 * g);
-  }
+template <int J, bool FULL, bool UNIT>
+__device__ __forceinline__ void softmax_row(float4 (&e)[J], int G, float sc, int float_sum) {
+  const int lane = threadIdx.x % kWave;
   float mx = -__builtin_inff();
 #pragma unroll
   for (int j = 0; j < J; j++) {
@@ -1137,11 +1126,44 @@ __global__ void __launch_bounds__(256) soft_max_rows_k(int64_t rows, int cols, f
     part[j] = (FULL || g < G) ? (e[j].x + e[j].y) + (e[j].z + e[j].w) : 0.0f;
   }
   const float inv = softmax_inv<J, FULL>(part, G, 0.0f, 0, float_sum);
+#pragma unroll
+  for (int j = 0; j < J; j++) e[j] = make_float4(e[j].x * inv, e[j].y * inv, e[j].z * inv, e[j].w * inv);
+}
+
+// ggml soft_max, one wave per row.  Lane l owns the four-element groups
+// g = l + 64j, loaded as float4 (coalesced).  Loads and stores are both
+// nontemporal: ordinary loads keep the logits in the MALL across back-to-back
+// calls of softmax alone (4.8 us instead of 5.6 on [4096,1024]) but evict the
+// data of the kernels around it (the config-2 module, softmax then a 64 Mi
+// GELU, ran 97 us per call instead of 89).  The row maximum is a wave reduction of v_max_f32: on rows without
+// NaN it equals ggml's (mx > w ? mx : w) chain in any order, and a +0/-0 tie
+// cannot change an output since exp(x - (+0)) = exp(x - (-0)); a NaN anywhere
+// in a row makes every output NaN through the sum, whatever the maximum.
+// Each group's e = ggml_v_expf(x*sc - mx) stays in registers, its
+// vaddvq_f32 part goes into softmax_inv, and y = e*inv (softmax_row).
+// FULL: every lane owns exactly J groups (cols == 256*J), so no group index
+// needs a bounds check.  UNIT: scale == 1, so x*sc is x (a NaN x makes the
+// whole row NaN either way, through its own part of the sum).
+template <int J, bool FULL, bool UNIT = false>
+__global__ void __launch_bounds__(256) soft_max_rows_k(int64_t rows, int cols, float sc, int float_sum,
+                                                       const float *__restrict__ X, float *__restrict__ Y) {
+  const int wave = threadIdx.x / kWave, lane = threadIdx.x % kWave;
+  const int G = cols / 4;
+  const int64_t row = blockIdx.x * 4LL + wave;
+  if (row >= rows) return;  // the whole wave; no barrier follows
+  const float *x = X + row * cols;
+  float4 e[J];
+#pragma unroll
+  for (int j = 0; j < J; j++) {
+    const int g = lane + kWave * j;
+    e[j] = (FULL || g < G) ? ld4_nt(x + 4 * g) : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+  }
+  softmax_row<J, FULL, UNIT>(e, G, sc, float_sum);
   float *y = Y + row * cols;
 #pragma unroll
   for (int j = 0; j < J; j++) {
     const int g = lane + kWave * j;
-    if (FULL || g < G) st4_nt(y + 4 * g, make_float4(e[j].x * inv, e[j].y * inv, e[j].z * inv, e[j].w * inv));
+    if (FULL || g < G) st4_nt(y + 4 * g, e[j]);
   }
 }
 
@@ -1211,6 +1233,238 @@ __global__ void __launch_bounds__(256) soft_max_tail_k(int64_t rows, int cols, f
     }
   }
   if (lane < T) y[4 * G + lane] = et * inv;
+}
+
+// ---- fused attention: S = Q K^T, its element-wise chain, ggml.soft_max, O = P V ----------
+//
+// One workgroup per (batch, 32 query rows): S and then P stay in LDS, so the
+// score matrix never goes through HBM.  Every value is the one the separate
+// kernels give: S in ggml_vec_dot_f32 order then the fused chain (the same
+// f32_binary), each row through softmax_row (the soft_max kernel's code), and
+// O in ggml order again.
+//
+// The products run on v_mfma_f32_16x16x1_4b_f32 (K = 1: one fused
+// multiply-add per output per instruction, as the 32x32 form): lane l
+// supplies A and B of block l / 16, row / column l % 16, and block b's output
+// (i, j) lands in lane j + 16 (i / 4), register 4 b + i % 4.  Lane l of block
+// bl = l / 16 supplies the k-quad 16 blk + 4 bl .. + 3 and instruction g its
+// component g, so block b of accumulator set g holds chain 4 b + g: an
+// output's 16 chains are registers r, 4 + r, 8 + r, 12 + r (r = i % 4) of the
+// four sets, in one lane, and ggml's tree needs no exchange (tree16).
+typedef float v16f __attribute__((ext_vector_type(16)));
+
+__device__ __forceinline__ v16f mfma16(float a, float b, const v16f &c) {
+  return __builtin_amdgcn_mfma_f32_16x16x1f32(a, b, c, 0, 0, 0);
+}
+
+// dot_finish's GGML_F32x4_REDUCE and vaddvq_f32 on a lane's four outputs.
+__device__ __forceinline__ void tree16(const v16f (&acc)[4], float (&out)[4]) {
+#pragma unroll
+  for (int r = 0; r < 4; r++) {
+    float w[4];
+#pragma unroll
+    for (int g = 0; g < 4; g++) {
+      const float u = acc[g][r] + acc[g][8 + r];       // sum[0] += sum[2]
+      const float v = acc[g][4 + r] + acc[g][12 + r];  // sum[1] += sum[3]
+      w[g] = u + v;                                    // sum[0] += sum[1]
+    }
+    out[r] = (w[0] + w[1]) + (w[2] + w[3]);  // vaddvq_f32
+  }
+}
+
+// The 16 instructions of one 16x16 tile over a k-range of 64 (four blocks),
+// A and B float4 k-quads per block; the first block of a product starts from
+// the inline +0 accumulator, as ggml's accumulators do.
+__device__ __forceinline__ void mfma16_block(v16f (&acc)[4], const float4 &a, const float4 &b, bool first) {
+  const v16f z = {};
+  acc[0] = mfma16(a.x, b.x, first ? z : acc[0]);
+  acc[1] = mfma16(a.y, b.y, first ? z : acc[1]);
+  acc[2] = mfma16(a.z, b.z, first ? z : acc[2]);
+  acc[3] = mfma16(a.w, b.w, first ? z : acc[3]);
+}
+
+constexpr int kAttnRows = 32;  // query rows per workgroup
+constexpr int kAttnDh = 64;    // head dim (the Q K^T contraction)
+constexpr int kAttnDv = 64;    // value columns
+
+// J = keys / 256.  Q (b, n, d) and K (b, m, d) along d (16-byte aligned rows),
+// V (b, m, e) along e; O [B, NQ, 64] contiguous.  Wave w computes S for key
+// tiles w, w + 4, ... (both query tiles), softmax for rows 8 w .. 8 w + 7, and
+// O for value columns 16 w .. 16 w + 15 (both query tiles).
+template <int J, bool UNIT>
+__global__ void __launch_bounds__(256, 2) attention_k(MfmaOperand Q, MfmaOperand Kk, MfmaOperand V, int64_t NQ,
+                                                      Epilogue e1, float sm_sc, Epilogue e2,
+                                                      float *__restrict__ O) {
+  constexpr int NK = 256 * J, KT = NK / 16, LS = NK + 4;  // rows 4 floats apart: the writes spread over banks
+  __shared__ __attribute__((aligned(16))) float S[kAttnRows * LS];
+  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave: an SGPR
+  const int bl = lane >> 4, li = lane & 15;
+  // Consecutive query blocks of one batch share K and V: each XCD takes a
+  // contiguous run of workgroups (whole batches), whose K and V stay in its L2.
+  uint32_t tx = blockIdx.x, ty = blockIdx.y;
+  if (gridDim.y > 1) xcd_tile(tx, ty);
+  const int64_t b = ty, n0 = (int64_t)tx * kAttnRows;
+
+  // ---- S = Q K^T, then the chain, into LDS --------------------------------------
+  // K and V load through buffer resources: one 32-bit per-lane byte offset
+  // for the whole kernel, every per-tile and per-block advance in the scalar
+  // offset (each batch's K and V slices are below 2^31 bytes: the host checks).
+  const float *qb = Q.p + boff(Q, b);
+  const __amdgpu_buffer_rsrc_t kr =
+      __builtin_amdgcn_make_buffer_rsrc((void *)(Kk.p + boff(Kk, b)), (short)0, 0x7FFFFFFF, 0x00020000);
+  const int kvo = (int)(((int64_t)(16 * wave + li) * Kk.sf + 4 * bl) * 4);
+  auto kload = [&](int kt, int blk) {
+    return buf_ld4(BufOp{kr, kvo, nullptr}, (int)((int64_t)16 * (kt - wave) * Kk.sf * 4 + 64 * blk));
+  };
+  float4 qa[2][4];
+#pragma unroll
+  for (int qt = 0; qt < 2; qt++)
+#pragma unroll
+    for (int blk = 0; blk < 4; blk++) qa[qt][blk] = ld4(qb + (n0 + 16 * qt + li) * Q.sf + 16 * blk + 4 * bl);
+  auto qk_tile = [&](const float4 (&ks)[4], int kt) {
+    const int64_t m = 16 * kt + li;
+#pragma unroll
+    for (int qt = 0; qt < 2; qt++) {
+      v16f acc[4];
+#pragma unroll
+      for (int blk = 0; blk < 4; blk++) mfma16_block(acc, qa[qt][blk], ks[blk], blk == 0);
+      float out[4];
+      tree16(acc, out);
+#pragma unroll
+      for (int r = 0; r < 4; r++) S[(16 * qt + 4 * bl + r) * LS + m] = out[r];
+    }
+  };
+  // Key tiles in two register sets that take turns (a wave's KT / 4 tiles
+  // are an even count): one set's loads fly while the other's products run.
+  float4 ka[4], kc[4];
+#pragma unroll
+  for (int blk = 0; blk < 4; blk++) ka[blk] = kload(wave, blk);
+#pragma unroll 1
+  for (int kt = wave; kt < KT; kt += 8) {
+#pragma unroll
+    for (int blk = 0; blk < 4; blk++) kc[blk] = kload(kt + 4, blk);
+    qk_tile(ka, kt);
+    const int kn = kt + 8 < KT ? kt + 8 : kt;  // past the end: reloads, in bounds
+#pragma unroll
+    for (int blk = 0; blk < 4; blk++) ka[blk] = kload(kn, blk);
+    qk_tile(kc, kt + 4);
+  }
+  __syncthreads();
+
+  // ---- the chain on S, then P = softmax(S), by rows in place ------------------------
+  // The chain's ops (the same f32_binary, in order, per element) run here
+  // rather than after each product tile: a row's operands (a mask row) load
+  // as coalesced float4s, the next row's while this one is computed.
+  // Operand r of a lane's row holds element 4 (lane + 64 (r / 4)) + r % 4.
+  auto chain_off = [&](const EpiOp &o, int row, int r) {
+    return b * o.s0 + (n0 + row) * o.s1 + (int64_t)(4 * (lane + kWave * (r / 4)) + r % 4) * o.s2;
+  };
+  auto chain_load = [&](int row, float (&w)[kEpiEarly][4 * J]) {
+#pragma unroll
+    for (int k = 0; k < kEpiEarly; k++) {
+      if (k >= e1.n) break;
+      const EpiOp &o = e1.op[k];
+      if (o.s2 == 0) {  // one value over the row
+        const float w0 = o.p[chain_off(o, row, 0)];
+#pragma unroll
+        for (int r = 0; r < 4 * J; r++) w[k][r] = w0;
+      } else if (o.s2 == 1 && (((uintptr_t)(o.p + chain_off(o, row, 0))) & 15) == 0) {
+#pragma unroll
+        for (int j = 0; j < J; j++) {
+          const float4 q = ld4(o.p + chain_off(o, row, 4 * j));
+          w[k][4 * j] = q.x, w[k][4 * j + 1] = q.y, w[k][4 * j + 2] = q.z, w[k][4 * j + 3] = q.w;
+        }
+      } else {
+#pragma unroll
+        for (int r = 0; r < 4 * J; r++) w[k][r] = o.p[chain_off(o, row, r)];
+      }
+    }
+  };
+  float wn[kEpiEarly][4 * J];
+  chain_load(8 * wave, wn);
+#pragma unroll 1
+  for (int rr = 0; rr < kAttnRows / 4; rr++) {
+    const int ri = 8 * wave + rr;
+    float *row = S + ri * LS;
+    float wc[kEpiEarly][4 * J];
+#pragma unroll
+    for (int k = 0; k < kEpiEarly; k++)
+#pragma unroll
+      for (int r = 0; r < 4 * J; r++) wc[k][r] = wn[k][r];
+    if (rr + 1 < kAttnRows / 4) chain_load(ri + 1, wn);
+    float v[4 * J];
+#pragma unroll
+    for (int j = 0; j < J; j++) {
+      const float4 q = *reinterpret_cast<const float4 *>(row + 4 * (lane + kWave * j));
+      v[4 * j] = q.x, v[4 * j + 1] = q.y, v[4 * j + 2] = q.z, v[4 * j + 3] = q.w;
+    }
+    epi_ops_n(e1, v, wc);
+    epi_apply_n(e1, v, [&](const EpiOp &o, int r) { return chain_off(o, ri, r); }, kEpiEarly);
+    float4 e[J];
+#pragma unroll
+    for (int j = 0; j < J; j++) e[j] = make_float4(v[4 * j], v[4 * j + 1], v[4 * j + 2], v[4 * j + 3]);
+    softmax_row<J, true, UNIT>(e, 64 * J, sm_sc, 0);
+#pragma unroll
+    for (int j = 0; j < J; j++) *reinterpret_cast<float4 *>(row + 4 * (lane + kWave * j)) = e[j];
+  }
+  __syncthreads();
+
+  // ---- O = P V: value columns 16 wave .., both query tiles -------------------------
+  const __amdgpu_buffer_rsrc_t vr =
+      __builtin_amdgcn_make_buffer_rsrc((void *)(V.p + boff(V, b)), (short)0, 0x7FFFFFFF, 0x00020000);
+  int vo[4];  // the lane's byte offsets of keys 4 bl + g, column 16 wave + li
+#pragma unroll
+  for (int g = 0; g < 4; g++) vo[g] = (int)(((int64_t)(16 * wave + li) * V.sf + (int64_t)(4 * bl + g) * V.sk) * 4);
+  const int vstep = (int)((int64_t)16 * V.sk * 4);  // one block of 16 keys
+  auto vload = [&](int blk) {
+    float r[4];
+#pragma unroll
+    for (int g = 0; g < 4; g++)
+      r[g] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(vr, vo[g], blk * vstep, 0));
+    return make_float4(r[0], r[1], r[2], r[3]);
+  };
+  auto pload = [&](int qt, int blk) {
+    return *reinterpret_cast<const float4 *>(S + (16 * qt + li) * LS + 16 * blk + 4 * bl);
+  };
+  // V's operands load four blocks ahead of their products, in two register
+  // sets that take turns (NK / 16 is a multiple of 8): the loads of one set
+  // fly while the other feeds the MFMAs, and no register moves between them.
+  constexpr int NB = NK / 16;
+  v16f acc[2][4];
+#pragma unroll
+  for (int qt = 0; qt < 2; qt++)
+#pragma unroll
+    for (int g = 0; g < 4; g++) acc[qt][g] = v16f{};
+  auto pv4 = [&](const float4 (&vs)[4], int blk0) {
+#pragma unroll
+    for (int i = 0; i < 4; i++)
+#pragma unroll
+      for (int qt = 0; qt < 2; qt++) mfma16_block(acc[qt], pload(qt, blk0 + i), vs[i], false);
+  };
+  float4 va[4], vb[4];
+#pragma unroll
+  for (int i = 0; i < 4; i++) va[i] = vload(i);
+#pragma unroll 1
+  for (int b0 = 0; b0 < NB; b0 += 8) {
+#pragma unroll
+    for (int i = 0; i < 4; i++) vb[i] = vload(b0 + 4 + i);
+    pv4(va, b0);
+#pragma unroll
+    for (int i = 0; i < 4; i++) va[i] = vload(min(b0 + 8 + i, NB - 1));  // past the end: reloads, in bounds
+    pv4(vb, b0 + 4);
+  }
+  const int64_t d = 16 * wave + li;
+#pragma unroll
+  for (int qt = 0; qt < 2; qt++) {
+    float out[4];
+    tree16(acc[qt], out);
+    const int64_t nq = n0 + 16 * qt + 4 * bl;
+    epi_apply_n(e2, out, [&](const EpiOp &o, int r) { return b * o.s0 + (nq + r) * o.s1 + d * o.s2; }, 0, NoUnary(),
+                DotUniform<true>());
+    float *y = O + (b * NQ + nq) * kAttnDv + d;
+#pragma unroll
+    for (int r = 0; r < 4; r++) y[r * kAttnDv] = out[r];
+  }
 }
 
 // ---- rows longer than 4096 columns -------------------------------------------------
@@ -2015,6 +2269,55 @@ ArrayP dot_ggml(const DotOperand &lhs, const DotOperand &rhs, int64_t B, int64_t
         dot_ggml_simple<kTailPlain><<<grid, 256, 0, s>>>(n_out, N, M, K, X, W, ep, Y);
         break;
     }
+  });
+  return y;
+}
+
+ArrayP attention_ggml(const DotOperand &q, const DotOperand &k, const DotOperand &v, int64_t B, int64_t NQ,
+                      int64_t NK, int64_t DH, int64_t DV, const std::vector<FusedOp> &epi1, uint32_t sm_scale_bits,
+                      const std::vector<FusedOp> &epi2) {
+  for (const DotOperand *d : {&q, &k, &v})
+    if (d->arr->dtype != kF32 || !d->arr->buf || d->nb2 < 1 || B % d->nb2) return nullptr;
+  if (DH != kAttnDh || DV != kAttnDv || NK % 256 || NK < 256 || NK > 1024 || NQ <= 0 || NQ % kAttnRows) return nullptr;
+  if (B < 1 || B > 65535 || NQ / kAttnRows > 0x7FFFFFFF) return nullptr;
+  auto rows_ok = [&](const DotOperand &d) {  // float4 loads along d from 16-byte aligned rows
+    const float *p = (const float *)d.arr->data();
+    return d.sk == 1 && d.sf % 4 == 0 && (uintptr_t)p % 16 == 0 && (d.sb % 4 == 0 || B == 1) &&
+           (d.nb2 == 1 || d.sb2 % 4 == 0);
+  };
+  if (!rows_ok(q) || !rows_ok(k) || v.sf != 1) return nullptr;
+  // K's and V's buffer offsets within a batch stay below 2^31 bytes
+  if (((NK - 1) * k.sf + DH) * 4 >= ((int64_t)1 << 31) || (DV + (NK + 16) * v.sk) * 4 >= ((int64_t)1 << 31) ||
+      k.sf < 0 || v.sk < 0)
+    return nullptr;
+  for (auto *ep : {&epi1, &epi2})
+    for (const FusedOp &o : *ep)
+      if (o.code == kEpiGeluErf) return nullptr;
+  std::vector<ArrayP> keep;
+  const Epilogue e1 = make_epilogue(epi1, &keep), e2 = make_epilogue(epi2, &keep);
+  auto y = new_array(kF32, Shape{B * NQ * DV});
+  const MfmaOperand Q{(const float *)q.arr->data(), q.sb, q.sf, q.sk, NQ, q.sb2, q.nb2};
+  const MfmaOperand Kk{(const float *)k.arr->data(), k.sb, k.sf, k.sk, NK, k.sb2, k.nb2};
+  const MfmaOperand V{(const float *)v.arr->data(), v.sb, v.sf, v.sk, DV, v.sb2, v.nb2};
+  float *Y = (float *)y->data();
+  const float sc = bits_f(sm_scale_bits);
+  const bool unit = sm_scale_bits == 0x3F800000u;
+  const dim3 grid((unsigned)(NQ / kAttnRows), (unsigned)B);
+  const int J = (int)(NK / 256);
+  ArrayP kq = q.arr, kk = k.arr, kvv = v.arr;
+  g_last_dot = strf("attention_k<%d>", J);
+  launch([=](hipStream_t s) {
+    (void)kq, (void)kk, (void)kvv, (void)keep;
+#define ATT_CASE(j)                                                                                  \
+  case j:                                                                                            \
+    if (unit) attention_k<j, true><<<grid, 256, 0, s>>>(Q, Kk, V, NQ, e1, sc, e2, Y);                \
+    else attention_k<j, false><<<grid, 256, 0, s>>>(Q, Kk, V, NQ, e1, sc, e2, Y);                    \
+    break;
+    switch (J) {
+      ATT_CASE(1) ATT_CASE(2) ATT_CASE(3) ATT_CASE(4)
+      default: break;
+    }
+#undef ATT_CASE
   });
   return y;
 }

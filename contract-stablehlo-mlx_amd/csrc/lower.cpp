@@ -625,10 +625,19 @@ struct Lowerer {
   // applies the chain to each output before storing it.  Each op is one IEEE
   // rounding of the same operands, so the bits are those of the separate ops.
 
+  // An attention group: S = dot_general(q, k) with its chain, P = ggml.soft_max(S),
+  // O = dot_general(P, v) with its chain, run by attention_ggml when it carries them.
+  struct AttnGroup {
+    int qk = -1, sm = -1, pv = -1;
+    std::vector<int> ch1, ch2;
+  };
+
   struct Fusion {
     std::vector<char> skip;               // the producer and the chain's inner ops
     std::vector<int> producer;            // at a chain's last op: its producer's index
     std::vector<std::vector<int>> chain;  // at a producer: its chain's op indices
+    std::vector<int> attn;                // at an attention group's last op: the group's index
+    std::vector<AttnGroup> groups;
   };
 
   static void count_uses(const Block &b, std::unordered_map<std::string, int> *uses) {
@@ -682,7 +691,8 @@ struct Lowerer {
 
   Fusion plan_fusion(const Block &b) const {
     const size_t n = b.ops.size();
-    Fusion fu{std::vector<char>(n, 0), std::vector<int>(n, -1), std::vector<std::vector<int>>(n)};
+    Fusion fu{std::vector<char>(n, 0), std::vector<int>(n, -1), std::vector<std::vector<int>>(n),
+              std::vector<int>(n, -1), {}};
     std::unordered_map<std::string, int> uses, user;
     count_uses(b, &uses);
     for (size_t k = 0; k < n; k++)
@@ -710,12 +720,56 @@ struct Lowerer {
       fu.producer[ch.back()] = (int)i;
       fu.chain[i] = ch;
     }
+    plan_attention(b, uses, user, &fu);
     return fu;
   }
 
-  std::vector<ArrayP> run_fused(const Env &env, const std::vector<Op> &ops, int p, const std::vector<int> &ch) {
-    const Op &d = ops[p];
-    std::string cur = d.results[0];
+  // Attention groups among the planned chains: a dot_general (with its chain)
+  // whose value's one use is a ggml.soft_max, whose result's one use is the
+  // lhs of a dot_general (with its chain).  Not under the planted faults that
+  // change a product or the softmax (the separate kernels carry those).
+  void plan_attention(const Block &b, std::unordered_map<std::string, int> &uses,
+                      const std::unordered_map<std::string, int> &user, Fusion *fu) const {
+    if (f.dot_builtin || f.dot_plain || f.soft_max_float_sum) return;
+    const size_t n = b.ops.size();
+    auto one_user = [&](const std::string &v, int after) -> int {
+      if (uses[v] != 1) return -1;
+      auto it = user.find(v);
+      return it == user.end() || it->second <= after ? -1 : it->second;
+    };
+    for (size_t i = 0; i < n; i++) {
+      const Op &qk = b.ops[i];
+      if (qk.name != "stablehlo.dot_general" || !fusable_producer(qk) || fu->attn[i] >= 0) continue;
+      const std::vector<int> &ch1 = fu->chain[i];
+      const int end1 = ch1.empty() ? (int)i : ch1.back();
+      const int s = one_user(b.ops[end1].results[0], end1);
+      if (s < 0) continue;
+      const Op &sm = b.ops[s];
+      if ((sm.name != "stablehlo.custom_call" && sm.name != "stablehlo.composite") ||
+          composite_name(sm) != "ggml.soft_max" || sm.operands.size() != 1 || sm.results.size() != 1 ||
+          sm.out_tys.size() != 1 || sm.out_tys[0].el != "f32")
+        continue;
+      const int p = one_user(sm.results[0], s);
+      if (p < 0) continue;
+      const Op &pv = b.ops[p];
+      if (pv.name != "stablehlo.dot_general" || !fusable_producer(pv) || pv.operands[0] != sm.results[0] ||
+          pv.operands[1] == sm.results[0] || fu->skip[p] && fu->chain[p].empty())
+        continue;
+      AttnGroup g{(int)i, s, p, ch1, fu->chain[p]};
+      const int last = g.ch2.empty() ? p : g.ch2.back();
+      fu->skip[i] = 1;
+      for (int k : g.ch1) fu->skip[k] = 1, fu->producer[k] = -1;
+      fu->skip[s] = 1;
+      fu->skip[p] = p != last;
+      fu->producer[last] = -1;
+      fu->skip[last] = 0;
+      fu->attn[last] = (int)fu->groups.size();
+      fu->groups.push_back(std::move(g));
+    }
+  }
+
+  std::vector<Chained> chain_of(const Env &env, const std::vector<Op> &ops, int p, const std::vector<int> &ch) {
+    std::string cur = ops[p].results[0];
     std::vector<Chained> chain;
     for (int k : ch) {
       const Op &e = ops[k];
@@ -730,6 +784,65 @@ struct Lowerer {
       chain.push_back(Chained{c, rev, get(env, e.operands[rev ? 0 : 1])});
       cur = e.results[0];
     }
+    return chain;
+  }
+
+  // The fused attention kernel when it carries the group's shapes and
+  // layouts, else the group's ops one by one (the same bits either way).
+  std::vector<ArrayP> run_attention(const Env &env, const std::vector<Op> &ops, const AttnGroup &g) {
+    const Op &qk = ops[g.qk], &sm = ops[g.sm], &pv = ops[g.pv];
+    const ArrayP q = get(env, qk.operands.at(0)), k = get(env, qk.operands.at(1)), v = get(env, pv.operands.at(1));
+    const std::vector<Chained> c1 = chain_of(env, ops, g.qk, g.ch1), c2 = chain_of(env, ops, g.pv, g.ch2);
+    const Ty &st = qk.out_tys.at(0), &ot = pv.out_tys.at(0);
+    const std::string attrs = attr_or(sm, "composite_attributes", attr_or(sm, "backend_config", ""));
+    const uint32_t scale = f32_attr(attrs, "scale");
+    std::vector<int64_t> lb, rb, lc, rc, lb2, rb2, lc2, rc2;
+    if (dot_dims(qk, &lb, &rb, &lc, &rc) && dot_dims(pv, &lb2, &rb2, &lc2, &rc2) && sm.out_tys[0].dims == st.dims &&
+        q->shape == qk.in_tys.at(0).dims && k->shape == qk.in_tys.at(1).dims && v->shape == pv.in_tys.at(1).dims) {
+      const Ty &ta = qk.in_tys[0], &tb = qk.in_tys[1], &tv = pv.in_tys[1];
+      auto contains = [](const std::vector<int64_t> &x, int64_t d) { return std::find(x.begin(), x.end(), d) != x.end(); };
+      auto prod = [](const Ty &t, const std::vector<int64_t> &ds) {
+        int64_t m = 1;
+        for (int64_t d : ds) m *= t.dims.at(d);
+        return m;
+      };
+      std::vector<int64_t> lf, rf, vf;
+      for (int64_t d = 0; d < (int64_t)ta.dims.size(); d++)
+        if (!contains(lb, d) && !contains(lc, d)) lf.push_back(d);
+      for (int64_t d = 0; d < (int64_t)tb.dims.size(); d++)
+        if (!contains(rb, d) && !contains(rc, d)) rf.push_back(d);
+      for (int64_t d = 0; d < (int64_t)tv.dims.size(); d++)
+        if (!contains(rb2, d) && !contains(rc2, d)) vf.push_back(d);
+      const int64_t nb = (int64_t)lb.size(), nl = (int64_t)lf.size(), rank = (int64_t)st.dims.size();
+      // P's batch dims are S's, in order; P contracts its last dim, the one key dim.
+      std::vector<int64_t> sb(nb);
+      for (int64_t d = 0; d < nb; d++) sb[d] = d;
+      const int64_t B = prod(ta, lb), NQ = prod(ta, lf), NK = prod(tb, rf), DH = ta.dims.at(lc[0]);
+      if (rf.size() == 1 && lb2 == sb && lc2.size() == 1 && lc2[0] == rank - 1 && rank == nb + nl + 1 &&
+          tv.dims.at(rc2[0]) == NK && prod(tv, rb2) == B && tb.dims.at(rc[0]) == DH && prod(tb, rb) == B) {
+        std::vector<int64_t> g1[3], g2[3];
+        for (int64_t d = 0; d < rank; d++) g1[d < nb ? 0 : d < nb + nl ? 1 : 2].push_back(d);
+        for (int64_t d = 0; d < (int64_t)ot.dims.size(); d++) g2[d < nb ? 0 : d < nb + nl ? 1 : 2].push_back(d);
+        const std::vector<FusedOp> e1 = fusable_prefix(c1, st.dims, g1, false);
+        const std::vector<FusedOp> e2 = fusable_prefix(c2, ot.dims, g2, false);
+        if (e1.size() == c1.size()) {
+          const DotOperand Q = dot_operand(q, lb, lf, lc[0]), K = dot_operand(k, rb, rf, rc[0]);
+          const DotOperand V = dot_operand(v, rb2, vf, rc2[0]);
+          if (ArrayP y = attention_ggml(Q, K, V, B, NQ, NK, DH, prod(tv, vf), e1, scale, e2))
+            return {apply_chain(reshape(y, ot.dims), c2, e2.size())};
+        }
+      }
+    }
+    ArrayP s = dot_general(f, qk, q, k, c1);
+    const auto rcs = rows_cols(sm.out_tys[0]);
+    require_tail_expf("ggml.soft_max", rcs.second);
+    ArrayP pr = reshape(soft_max(s, rcs.first, rcs.second, scale, f.soft_max_float_sum), sm.out_tys[0].dims);
+    return {dot_general(f, pv, pr, v, c2)};
+  }
+
+  std::vector<ArrayP> run_fused(const Env &env, const std::vector<Op> &ops, int p, const std::vector<int> &ch) {
+    const Op &d = ops[p];
+    const std::vector<Chained> chain = chain_of(env, ops, p, ch);
     if (d.name == "stablehlo.dot_general")
       return {dot_general(f, d, get(env, d.operands.at(0)), get(env, d.operands.at(1)), chain)};
     return {run_norm(d, get(env, d.operands.at(0)), chain)};
@@ -750,8 +863,9 @@ struct Lowerer {
     for (size_t i = 0; i < b.ops.size(); i++) {
       const Op &o = b.ops[i];
       if (fu.skip[i]) continue;  // a fused producer or inner chain op: runs with the chain's last op
-      auto rs = fu.producer[i] >= 0 ? run_fused(env, b.ops, fu.producer[i], fu.chain[fu.producer[i]])
-                                    : run_op(env, known, o);
+      auto rs = fu.attn[i] >= 0        ? run_attention(env, b.ops, fu.groups[fu.attn[i]])
+                : fu.producer[i] >= 0 ? run_fused(env, b.ops, fu.producer[i], fu.chain[fu.producer[i]])
+                                      : run_op(env, known, o);
       if (rs.size() != o.results.size())
         fail(strf("%s: %zu results for %zu names", o.name.c_str(), rs.size(), o.results.size()));
       for (size_t j = 0; j < rs.size(); j++) env[o.results[j]] = rs[j];

@@ -98,6 +98,17 @@ struct FusedOp {
 ArrayP dot_ggml(const DotOperand &lhs, const DotOperand &rhs, int64_t B, int64_t N, int64_t M,
                 int64_t K, int tail, const std::vector<FusedOp> &epi = {});
 
+// softmax(chain1(Q K^T)) V in one kernel (S and P stay in LDS), for q, k
+// (b, query / key, d) and v (b, key, e) with DH = 64 head dims, DV = 64 value
+// columns, NK keys a multiple of 256 up to 1024 and NQ queries a multiple of
+// 32: the same bits as dot_ggml, its chain, soft_max and dot_ggml again.
+// chain2 applies to the output at (b, n, e).  Returns null when the shapes or
+// layouts are not carried (the caller runs the separate ops).  Output
+// [B*NQ*DV].
+ArrayP attention_ggml(const DotOperand &q, const DotOperand &k, const DotOperand &v, int64_t B, int64_t NQ,
+                      int64_t NK, int64_t DH, int64_t DV, const std::vector<FusedOp> &epi1, uint32_t sm_scale_bits,
+                      const std::vector<FusedOp> &epi2);
+
 // The kernel the last dot_ggml call chose, e.g. "dot_mfma8d_k<RowVecB,ColQuadB,128,8>"
 // (host bookkeeping for tests and profiles; "" before the first call).
 const std::string &last_dot_kernel();

@@ -1,0 +1,239 @@
+"""The fused attention kernel (attention_k): S = Q K^T with its element-wise
+chain, P = ggml.soft_max(S), O = P V in one kernel, S and P in LDS.
+
+The lowering runs a dot_general -> (chain) -> ggml.soft_max -> dot_general
+group through it when the shapes and layouts allow (head dim 64, 64 value
+columns, keys a multiple of 256 up to 1024, queries a multiple of 32), and
+through the separate kernels otherwise.  Either way every output bit must be
+the oracle's (dot in ggml order, the chain's IEEE ops, ggml soft_max, dot
+again): eager and compiled, graph-captured and replayed."""
+import numpy as np
+import pytest
+
+pytestmark = [pytest.mark.gpu, pytest.mark.usefixtures("graph_mode")]
+
+F32 = np.float32
+
+
+def t(shape):
+    return "tensor<" + "".join(f"{d}x" for d in shape) + "f32>"
+
+
+def hexf(x):
+    return "0x%08X" % int(np.array([x], F32).view(np.uint32)[0])
+
+
+def attn_module(B, H, NQ, NK, D=64, DV=64, scale=0.125, mask=True, sm_scale=1.0, residual=False):
+    q, k, v = t((B, H, NQ, D)), t((B, H, NK, D)), t((B, H, NK, DV))
+    s, o, m = t((B, H, NQ, NK)), t((B, H, NQ, DV)), t((NQ, NK))
+    qk = ("#stablehlo.dot<lhs_batching_dimensions = [0, 1], rhs_batching_dimensions = [0, 1], "
+          "lhs_contracting_dimensions = [3], rhs_contracting_dimensions = [3]>")
+    pv = ("#stablehlo.dot<lhs_batching_dimensions = [0, 1], rhs_batching_dimensions = [0, 1], "
+          "lhs_contracting_dimensions = [3], rhs_contracting_dimensions = [2]>")
+    args = [f"%q: {q}", f"%k: {k}", f"%v: {v}"] + ([f"%mask: {m}"] if mask else []) + ([f"%res: {o}"] if residual else [])
+    L = [f'    %0 = "stablehlo.dot_general"(%q, %k) {{dot_dimension_numbers = {qk}}} : ({q}, {k}) -> {s}']
+    cur = "%0"
+    if scale is not None:
+        L += [f'    %c = "stablehlo.constant"() {{value = dense<{hexf(scale)}> : tensor<f32>}} : () -> tensor<f32>',
+              f'    %cb = "stablehlo.broadcast_in_dim"(%c) {{broadcast_dimensions = array<i64>}} : (tensor<f32>) -> {s}',
+              f'    %1 = "stablehlo.multiply"({cur}, %cb) : ({s}, {s}) -> {s}']
+        cur = "%1"
+    if mask:
+        L += [f'    %mb = "stablehlo.broadcast_in_dim"(%mask) {{broadcast_dimensions = array<i64: 2, 3>}} : ({m}) -> {s}',
+              f'    %2 = "stablehlo.add"({cur}, %mb) : ({s}, {s}) -> {s}']
+        cur = "%2"
+    L += [f'    %3 = "stablehlo.custom_call"({cur}) {{call_target_name = "ggml.soft_max", '
+          f'backend_config = "scale = {hexf(sm_scale)} : f32"}} : ({s}) -> {s}',
+          f'    %4 = "stablehlo.dot_general"(%3, %v) {{dot_dimension_numbers = {pv}}} : ({s}, {v}) -> {o}']
+    ret = "%4"
+    if residual:
+        L += [f'    %5 = "stablehlo.add"(%res, %4) : ({o}, {o}) -> {o}']
+        ret = "%5"
+    body = "\n".join(L)
+    return (f"module {{\n  func.func public @main({', '.join(args)}) -> ({o}) {{\n{body}\n"
+            f"    func.return {ret} : {o}\n  }}\n}}\n")
+
+
+def inputs(oracle, B, H, NQ, NK, D=64, DV=64, seed=61):
+    q, st = oracle.fill_normal(seed, 1.0, B * H * NQ * D)
+    k, st = oracle.fill_normal(seed, 1.0, B * H * NK * D, state=st)
+    v, _ = oracle.fill_normal(seed, 1.0, B * H * NK * DV, state=st)
+    return q.reshape(B, H, NQ, D), k.reshape(B, H, NK, D), v.reshape(B, H, NK, DV)
+
+
+def causal(NQ, NK):
+    return np.where(np.triu(np.ones((NQ, NK), bool), 1 + NK - NQ), F32(-np.inf), F32(0))
+
+
+def oracle_attn(oracle, q, k, v, mask=None, scale=0.125, sm_scale=1.0, residual=None):
+    B, H, NQ, D = q.shape
+    NK, DV = k.shape[2], v.shape[3]
+    s = oracle.dot_general_bnk(q.reshape(B * H, NQ, D), k.reshape(B * H, NK, D))
+    if scale is not None:
+        s = (s * F32(scale)).astype(F32)
+    if mask is not None:
+        s = (s + mask[None]).astype(F32)
+    p = oracle.soft_max(s, scale=F32(sm_scale))
+    vt = np.ascontiguousarray(v.reshape(B * H, NK, DV).transpose(0, 2, 1))
+    o = oracle.dot_general_bnk(p, vt).reshape(B, H, NQ, DV)
+    if residual is not None:
+        o = (residual + o).astype(F32)
+    return o
+
+
+def bits_equal(a, b, nan_ok=False):
+    ua, ub = np.ascontiguousarray(a).view(np.uint32), np.ascontiguousarray(b).view(np.uint32)
+    if not nan_ok:
+        return a.shape == b.shape and np.array_equal(ua, ub)
+    na, nb = (ua & 0x7FFFFFFF) > 0x7F800000, (ub & 0x7FFFFFFF) > 0x7F800000
+    return a.shape == b.shape and np.array_equal(na, nb) and np.array_equal(ua[~na], ub[~nb])
+
+
+def run(text, ins, compile=True, faults=0):
+    import shlo_hip
+    m = shlo_hip.Module(text)
+    return m.prepare(faults, compile).call([shlo_hip.from_numpy(np.ascontiguousarray(x)) for x in ins])[0].numpy()
+
+
+@pytest.mark.parametrize("B,H,NQ,NK", [(2, 2, 256, 256), (1, 3, 512, 512), (2, 1, 96, 768), (1, 2, 64, 1024),
+                                       (3, 2, 160, 512)])
+def test_fused_attention_vs_oracle(oracle, B, H, NQ, NK):
+    import shlo_hip
+    q, k, v = inputs(oracle, B, H, NQ, NK)
+    mask = causal(NQ, NK)
+    want = oracle_attn(oracle, q, k, v, mask)
+    text = attn_module(B, H, NQ, NK)
+    for compile in (False, True):
+        got = run(text, [q, k, v, mask], compile=compile)
+        if not compile:
+            assert shlo_hip.last_dot_kernel() == f"attention_k<{NK // 256}>"
+        assert bits_equal(got, want), compile
+
+
+@pytest.mark.parametrize("variant", ["no_chain", "scale_only", "mask_only", "sm_scale_half", "residual"])
+def test_fused_attention_chain_variants(oracle, variant):
+    import shlo_hip
+    B, H, NQ, NK = 2, 2, 128, 512
+    q, k, v = inputs(oracle, B, H, NQ, NK, seed=62)
+    mask = causal(NQ, NK)
+    kw = dict(scale=0.125, mask=True, sm_scale=1.0, residual=False)
+    if variant == "no_chain":
+        kw.update(scale=None, mask=False)
+    elif variant == "scale_only":
+        kw.update(mask=False)
+    elif variant == "mask_only":
+        kw.update(scale=None)
+    elif variant == "sm_scale_half":
+        kw.update(sm_scale=0.5)
+    else:
+        kw.update(residual=True)
+    res, _ = oracle.fill_normal(63, 1.0, B * H * NQ * 64)
+    res = res.reshape(B, H, NQ, 64)
+    want = oracle_attn(oracle, q, k, v, mask if kw["mask"] else None, kw["scale"], kw["sm_scale"],
+                       res if kw["residual"] else None)
+    ins = [q, k, v] + ([mask] if kw["mask"] else []) + ([res] if kw["residual"] else [])
+    text = attn_module(B, H, NQ, NK, **kw)
+    for compile in (False, True):
+        got = run(text, ins, compile=compile)
+        if not compile:
+            assert shlo_hip.last_dot_kernel() == "attention_k<2>", variant
+        assert bits_equal(got, want), (variant, compile)
+
+
+def test_fused_attention_special_values(oracle):
+    """NaN and inf in Q, K and V rows, +-0, huge and subnormal scores, and
+    masked entries times an infinite V (0 * inf = NaN, which ggml keeps):
+    NaN outputs compared by NaN-ness, everything else bit for bit."""
+    import shlo_hip
+    B, H, NQ, NK = 1, 2, 64, 256
+    q, k, v = inputs(oracle, B, H, NQ, NK, seed=64)
+    q[0, 0, 3, 5] = np.nan
+    q[0, 1, 7, :] *= F32(1e18)  # huge scores: exp underflows to subnormal and zero probabilities
+    k[0, 0, 11, 2] = np.inf
+    k[0, 1, 40, :] = 0.0
+    k[0, 1, 41, :] = -0.0
+    v[0, 0, 200, 9] = np.inf  # masked for the early rows: 0 * inf
+    v[0, 1, 5, 3] = -np.inf
+    v[0, 1, 6, :] = F32(1e-40)
+    mask = causal(NQ, NK)
+    want = oracle_attn(oracle, q, k, v, mask)
+    text = attn_module(B, H, NQ, NK)
+    for compile in (False, True):
+        got = run(text, [q, k, v, mask], compile=compile)
+        if not compile:
+            assert shlo_hip.last_dot_kernel() == "attention_k<1>"
+        assert bits_equal(got, want, nan_ok=True), compile
+    assert np.isnan(want).any() and np.isfinite(want).any()
+
+
+def heads_module(B, T, H):
+    """Q, K, V as per-head views of one [B, T, 3 H 64] projection (slice,
+    reshape, transpose: two-level batch strides), then QK^T * 1/8, softmax,
+    PV, as the denoiser builds its attention."""
+    d = H * 64
+    x, s3 = t((B, T, 3 * d)), None
+    hv, s, o = t((B, H, T, 64)), t((B, H, T, T)), t((B, H, T, 64))
+    L = []
+    for i, nm in enumerate("qkv"):
+        L.append(f'    %{nm}s = "stablehlo.slice"(%x) {{start_indices = array<i64: 0, 0, {i * d}>, limit_indices = '
+                 f'array<i64: {B}, {T}, {(i + 1) * d}>, strides = array<i64: 1, 1, 1>}} : ({x}) -> {t((B, T, d))}')
+        L.append(f'    %{nm}r = "stablehlo.reshape"(%{nm}s) : ({t((B, T, d))}) -> {t((B, T, H, 64))}')
+        L.append(f'    %{nm} = "stablehlo.transpose"(%{nm}r) {{permutation = array<i64: 0, 2, 1, 3>}} : '
+                 f'({t((B, T, H, 64))}) -> {hv}')
+    qk = ("#stablehlo.dot<lhs_batching_dimensions = [0, 1], rhs_batching_dimensions = [0, 1], "
+          "lhs_contracting_dimensions = [3], rhs_contracting_dimensions = [3]>")
+    pv = ("#stablehlo.dot<lhs_batching_dimensions = [0, 1], rhs_batching_dimensions = [0, 1], "
+          "lhs_contracting_dimensions = [3], rhs_contracting_dimensions = [2]>")
+    L += [f'    %0 = "stablehlo.dot_general"(%q, %k) {{dot_dimension_numbers = {qk}}} : ({hv}, {hv}) -> {s}',
+          f'    %c = "stablehlo.constant"() {{value = dense<0x3E000000> : tensor<f32>}} : () -> tensor<f32>',
+          f'    %cb = "stablehlo.broadcast_in_dim"(%c) {{broadcast_dimensions = array<i64>}} : (tensor<f32>) -> {s}',
+          f'    %1 = "stablehlo.multiply"(%0, %cb) : ({s}, {s}) -> {s}',
+          f'    %3 = "stablehlo.custom_call"(%1) {{call_target_name = "ggml.soft_max", '
+          f'backend_config = "scale = 0x3F800000 : f32"}} : ({s}) -> {s}',
+          f'    %4 = "stablehlo.dot_general"(%3, %v) {{dot_dimension_numbers = {pv}}} : ({s}, {hv}) -> {o}']
+    body = "\n".join(L)
+    return (f"module {{\n  func.func public @main(%x: {x}) -> ({o}) {{\n{body}\n"
+            f"    func.return %4 : {o}\n  }}\n}}\n")
+
+
+def test_fused_attention_head_views(oracle):
+    import shlo_hip
+    B, T, H = 2, 256, 3
+    x, _ = oracle.fill_normal(65, 1.0, B * T * 3 * H * 64)
+    x = x.reshape(B, T, 3 * H * 64)
+    heads = x.reshape(B, T, 3, H, 64).transpose(2, 0, 3, 1, 4)
+    q, k, v = (np.ascontiguousarray(heads[i]) for i in range(3))
+    want = oracle_attn(oracle, q, k, v)
+    for compile in (False, True):
+        got = run(heads_module(B, T, H), [x], compile=compile)
+        if not compile:
+            assert shlo_hip.last_dot_kernel() == "attention_k<1>"
+        assert bits_equal(got, want), compile
+
+
+@pytest.mark.parametrize("B,H,NQ,NK,D", [(2, 2, 128, 128, 64), (1, 2, 40, 256, 64), (1, 2, 64, 256, 40)])
+def test_unfused_attention_shapes(oracle, B, H, NQ, NK, D):
+    """Shapes the fused kernel does not carry (keys not a multiple of 256,
+    queries not a multiple of 32, head dim 40) run the separate kernels."""
+    import shlo_hip
+    q, k, v = inputs(oracle, B, H, NQ, NK, D=D, DV=64, seed=66)
+    mask = causal(NQ, NK)
+    want = oracle_attn(oracle, q, k, v, mask)
+    for compile in (False, True):
+        got = run(attn_module(B, H, NQ, NK, D=D), [q, k, v, mask], compile=compile)
+        if not compile:
+            assert shlo_hip.last_dot_kernel().startswith("dot_"), shlo_hip.last_dot_kernel()
+        assert bits_equal(got, want), compile
+
+
+def test_planted_faults_still_differ(oracle):
+    import shlo_hip
+    B, H, NQ, NK = 1, 2, 64, 256
+    q, k, v = inputs(oracle, B, H, NQ, NK, seed=67)
+    mask = causal(NQ, NK)
+    want = oracle_attn(oracle, q, k, v, mask)
+    text = attn_module(B, H, NQ, NK)
+    assert bits_equal(run(text, [q, k, v, mask]), want)
+    for fault in ("dot_plain", "dot_builtin", "soft_max_float_sum", "binary_half", "broadcast_first"):
+        got = run(text, [q, k, v, mask], faults=shlo_hip.fault_bits(fault))
+        assert not bits_equal(got, want), fault
