@@ -85,11 +85,19 @@ __device__ __forceinline__ float epi_apply(const Epilogue &e, float v, int64_t i
 // The fused ops on NV output values a lane holds: value r sits at element
 // offset off(op, r) of each op's operand (a producer clamps the offsets of
 // values it discards into range).  One uniform switch per op, then the op on
-// all NV values, their operand loads issued together.
+// all NV values, their operand loads issued together.  The operand order is
+// a branch around the whole loop, not a select per value.
+template <uint32_t C, bool REV, int NV>
+__device__ __forceinline__ void epi_op_in(float (&v)[NV], const float (&w)[NV]) {
+#pragma unroll
+  for (int r = 0; r < NV; r++) v[r] = REV ? f32_binary(C, w[r], v[r]) : f32_binary(C, v[r], w[r]);
+}
 template <uint32_t C, int NV>
 __device__ __forceinline__ void epi_op(float (&v)[NV], const float (&w)[NV], uint32_t rev) {
-#pragma unroll
-  for (int r = 0; r < NV; r++) v[r] = rev ? f32_binary(C, w[r], v[r]) : f32_binary(C, v[r], w[r]);
+  if (rev)
+    epi_op_in<C, true>(v, w);
+  else
+    epi_op_in<C, false>(v, w);
 }
 
 // The same in two steps, for a producer that can issue the operand loads

@@ -1235,6 +1235,105 @@ __global__ void __launch_bounds__(256) soft_max_tail_k(int64_t rows, int cols, f
   if (lane < T) y[4 * G + lane] = et * inv;
 }
 
+// ---- softmax over 16-lane rows --------------------------------------------------------
+//
+// For rows of 64 NJ elements in LDS a wave takes four rows at once: lane
+// 16 q + i holds row q's four-element groups g = i + 16 j (j < NJ).  Every
+// reduction stays inside the row's 16 lanes (DPP), so the per-row work (the
+// maximum, the binary64 sum and its decision, the reciprocal) is shared by
+// four rows and needs no lane reads.  The values are softmax_row's.
+
+__device__ __forceinline__ float row16_max_f(float v) {
+  v = __builtin_fmaxf(v, bits_f((uint32_t)dpp_i<kDppXor1>((int)f_bits(v))));
+  v = __builtin_fmaxf(v, bits_f((uint32_t)dpp_i<kDppXor2>((int)f_bits(v))));
+  v = __builtin_fmaxf(v, bits_f((uint32_t)dpp_i<kDppHalfMirror>((int)f_bits(v))));
+  return __builtin_fmaxf(v, bits_f((uint32_t)dpp_i<kDppMirror>((int)f_bits(v))));
+}
+
+// fin(S) for the in-order binary64 sum S of a 16-lane row's parts (part[j]
+// of lane i is group i + 16 j), decided as in ordered_sum_apply: exact, or
+// inside an interval fin maps to one value (the sum's error over its NJ + 4
+// levels is far below 2^-40 of it: every part is >= 0), or else walked in
+// order, segment j (groups 16 j .. 16 j + 15) at a time.
+template <int NJ, class Fin>
+__device__ __forceinline__ float ordered_sum16(const float (&part)[NJ], Fin fin) {
+  double ls = 0.0;
+  int le = 255;
+#pragma unroll
+  for (int j = 0; j < NJ; j++) {
+    ls = ls + (double)part[j];
+    le = min(le, part_ulp_exp(part[j]));
+  }
+  ls = row16_sum(ls);
+  le = row16_min(le);
+  if (ls <= exact_limit(le)) return fin(ls);
+  const double d = ls * 0x1p-40;  // exact: ls >= 2^-149 or ls = 0
+  const float f_lo = fin(ls - d), f_hi = fin(ls + d);
+  if (f_lo == f_hi) return f_lo;  // false for NaN and infinity
+  const int base = threadIdx.x & 48;  // the row's first lane
+  double s = 0.0;
+#pragma unroll
+  for (int j = 0; j < NJ; j++) {
+    const double seg = row16_sum((double)part[j]);
+    const int sege = row16_min(part_ulp_exp(part[j]));
+    const double t = s + seg;
+    const double lim_p = exact_limit(sege);
+    const uint32_t hs = (uint32_t)(__builtin_bit_cast(uint64_t, s) >> 32);
+    const double lim_s = __builtin_bit_cast(double, (uint64_t)((hs & 0xFFF00000u) | 0x000FFFFEu) << 32);
+    if (t <= lim_p && (s == 0.0 || t <= lim_s)) {
+      s = t;
+    } else {
+#pragma unroll 1
+      for (int i = 0; i < 16; i++) s = s + (double)__shfl(part[j], base + i);
+    }
+  }
+  return fin(s);
+}
+
+// softmax_row on a 16-lane row of 16 NJ groups (every group present), the
+// row's values e also stored at rp (4 (i + 16 j) for group j): the rare
+// recomputation of the 126 < |n| <= 192 exponentials reads them back rather
+// than keeping the arguments in registers.
+template <int NJ, bool UNIT>
+__device__ __forceinline__ void softmax_row16(float4 (&e)[NJ], float sc, float *rp) {
+  const int li = threadIdx.x & 15;
+  float mx = -__builtin_inff();
+#pragma unroll
+  for (int j = 0; j < NJ; j++) {
+    *reinterpret_cast<float4 *>(rp + 4 * (li + 16 * j)) = e[j];
+    if (!UNIT) e[j] = make_float4(e[j].x * sc, e[j].y * sc, e[j].z * sc, e[j].w * sc);
+    mx = __builtin_fmaxf(mx, __builtin_fmaxf(__builtin_fmaxf(e[j].x, e[j].y), __builtin_fmaxf(e[j].z, e[j].w)));
+  }
+  mx = row16_max_f(mx);
+  bool mid = false;
+#pragma unroll
+  for (int j = 0; j < NJ; j++) {
+    bool m0, m1, m2, m3;
+    e[j].x = ggml_v_expf_nonpos(e[j].x - mx, &m0);
+    e[j].y = ggml_v_expf_nonpos(e[j].y - mx, &m1);
+    e[j].z = ggml_v_expf_nonpos(e[j].z - mx, &m2);
+    e[j].w = ggml_v_expf_nonpos(e[j].w - mx, &m3);
+    mid |= m0 | m1 | m2 | m3;
+  }
+  if (__any(mid)) {
+#pragma unroll
+    for (int j = 0; j < NJ; j++) {
+      float4 x = *reinterpret_cast<const float4 *>(rp + 4 * (li + 16 * j));
+      if (!UNIT) x = make_float4(x.x * sc, x.y * sc, x.z * sc, x.w * sc);
+      e[j].x = ggml_v_expf(x.x - mx);
+      e[j].y = ggml_v_expf(x.y - mx);
+      e[j].z = ggml_v_expf(x.z - mx);
+      e[j].w = ggml_v_expf(x.w - mx);
+    }
+  }
+  float part[NJ];
+#pragma unroll
+  for (int j = 0; j < NJ; j++) part[j] = (e[j].x + e[j].y) + (e[j].z + e[j].w);
+  const float inv = ordered_sum16<NJ>(part, [](double x) { return (float)(1.0 / x); });
+#pragma unroll
+  for (int j = 0; j < NJ; j++) e[j] = make_float4(e[j].x * inv, e[j].y * inv, e[j].z * inv, e[j].w * inv);
+}
+
 // ---- fused attention: S = Q K^T, its element-wise chain, ggml.soft_max, O = P V ----------
 //
 // One workgroup per (batch, 32 query rows): S and then P stay in LDS, so the
@@ -1288,74 +1387,92 @@ constexpr int kAttnDh = 64;    // head dim (the Q K^T contraction)
 constexpr int kAttnDv = 64;    // value columns
 
 // J = keys / 256.  Q (b, n, d) and K (b, m, d) along d (16-byte aligned rows),
-// V (b, m, e) along e; O [B, NQ, 64] contiguous.  Wave w computes S for key
-// tiles w, w + 4, ... (both query tiles), softmax for rows 8 w .. 8 w + 7, and
-// O for value columns 16 w .. 16 w + 15 (both query tiles).
-template <int J, bool UNIT>
-__global__ void __launch_bounds__(256, 2) attention_k(MfmaOperand Q, MfmaOperand Kk, MfmaOperand V, int64_t NQ,
-                                                      Epilogue e1, float sm_sc, Epilogue e2,
-                                                      float *__restrict__ O) {
-  constexpr int NK = 256 * J, KT = NK / 16, LS = NK + 4;  // rows 4 floats apart: the writes spread over banks
-  __shared__ __attribute__((aligned(16))) float S[kAttnRows * LS];
-  const int lane = threadIdx.x & 63, wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave: an SGPR
-  const int bl = lane >> 4, li = lane & 15;
-  // Consecutive query blocks of one batch share K and V: each XCD takes a
-  // contiguous run of workgroups (whole batches), whose K and V stay in its L2.
-  uint32_t tx = blockIdx.x, ty = blockIdx.y;
-  if (gridDim.y > 1) xcd_tile(tx, ty);
-  const int64_t b = ty, n0 = (int64_t)tx * kAttnRows;
+// V (b, m, e) along e; O [B, NQ, 64] contiguous.  A block is 32 query rows of
+// one batch; its score tile S, then P, is 32 rows of NK + 4 floats in LDS
+// (rows 4 floats apart: the writes spread over banks).  Three phases, each
+// split over four waves w = 0 .. 3: S for key tiles w, w + 4, ... (both query
+// tiles); the chain and softmax for eight of the rows; O for value columns
+// 16 w .. 16 w + 15 (both query tiles).
 
-  // ---- S = Q K^T, then the chain, into LDS --------------------------------------
-  // K and V load through buffer resources: one 32-bit per-lane byte offset
-  // for the whole kernel, every per-tile and per-block advance in the scalar
-  // offset (each batch's K and V slices are below 2^31 bytes: the host checks).
-  const float *qb = Q.p + boff(Q, b);
-  const __amdgpu_buffer_rsrc_t kr =
-      __builtin_amdgcn_make_buffer_rsrc((void *)(Kk.p + boff(Kk, b)), (short)0, 0x7FFFFFFF, 0x00020000);
-  const int kvo = (int)(((int64_t)(16 * wave + li) * Kk.sf + 4 * bl) * 4);
-  auto kload = [&](int kt, int blk) {
-    return buf_ld4(BufOp{kr, kvo, nullptr}, (int)((int64_t)16 * (kt - wave) * Kk.sf * 4 + 64 * blk));
-  };
+// K and V load through buffer resources: one 32-bit per-lane byte offset for
+// a whole phase, every per-tile and per-block advance in the scalar offset
+// (each batch's K and V slices are below 2^31 bytes: the host checks).
+__device__ __forceinline__ __amdgpu_buffer_rsrc_t attn_rsrc(const MfmaOperand &o, int64_t b) {
+  return __builtin_amdgcn_make_buffer_rsrc((void *)(o.p + boff(o, b)), (short)0, 0x7FFFFFFF, 0x00020000);
+}
+
+// Phase one's operands: the block's Q rows (both query tiles) and the first
+// key tile, loaded before the phase runs.
+struct AttnQk {
   float4 qa[2][4];
+  float4 ka[4];
+};
+
+__device__ __forceinline__ float4 attn_kload(const MfmaOperand &Kk, const __amdgpu_buffer_rsrc_t &kr, int wave,
+                                             int kt, int blk) {
+  const int lane = threadIdx.x & 63, bl = lane >> 4, li = lane & 15;
+  const int kvo = (int)(((int64_t)(16 * wave + li) * Kk.sf + 4 * bl) * 4);
+  return buf_ld4(BufOp{kr, kvo, nullptr}, (int)((int64_t)16 * (kt - wave) * Kk.sf * 4 + 64 * blk));
+}
+
+__device__ __forceinline__ void attn_qk_load(const MfmaOperand &Q, const MfmaOperand &Kk, int64_t b, int64_t n0,
+                                             int wave, AttnQk &st) {
+  const int lane = threadIdx.x & 63, bl = lane >> 4, li = lane & 15;
+  const float *qb = Q.p + boff(Q, b);
 #pragma unroll
   for (int qt = 0; qt < 2; qt++)
 #pragma unroll
-    for (int blk = 0; blk < 4; blk++) qa[qt][blk] = ld4(qb + (n0 + 16 * qt + li) * Q.sf + 16 * blk + 4 * bl);
+    for (int blk = 0; blk < 4; blk++) st.qa[qt][blk] = ld4(qb + (n0 + 16 * qt + li) * Q.sf + 16 * blk + 4 * bl);
+  const __amdgpu_buffer_rsrc_t kr = attn_rsrc(Kk, b);
+#pragma unroll
+  for (int blk = 0; blk < 4; blk++) st.ka[blk] = attn_kload(Kk, kr, wave, wave, blk);
+}
+
+// Phase one: S = Q K^T in ggml order.  Key tiles in two register sets that
+// take turns (a wave's KT / 4 tiles are an even count): one set's loads fly
+// while the other's products run.
+template <int J>
+__device__ __forceinline__ void attn_qk(const MfmaOperand &Kk, int64_t b, int wave, AttnQk &st, float *S) {
+  constexpr int NK = 256 * J, KT = NK / 16, LS = NK + 4;
+  const int lane = threadIdx.x & 63, bl = lane >> 4, li = lane & 15;
+  const __amdgpu_buffer_rsrc_t kr = attn_rsrc(Kk, b);
   auto qk_tile = [&](const float4 (&ks)[4], int kt) {
-    const int64_t m = 16 * kt + li;
+    const int m = 16 * kt + li;
 #pragma unroll
     for (int qt = 0; qt < 2; qt++) {
       v16f acc[4];
 #pragma unroll
-      for (int blk = 0; blk < 4; blk++) mfma16_block(acc, qa[qt][blk], ks[blk], blk == 0);
+      for (int blk = 0; blk < 4; blk++) mfma16_block(acc, st.qa[qt][blk], ks[blk], blk == 0);
       float out[4];
       tree16(acc, out);
 #pragma unroll
       for (int r = 0; r < 4; r++) S[(16 * qt + 4 * bl + r) * LS + m] = out[r];
     }
   };
-  // Key tiles in two register sets that take turns (a wave's KT / 4 tiles
-  // are an even count): one set's loads fly while the other's products run.
-  float4 ka[4], kc[4];
-#pragma unroll
-  for (int blk = 0; blk < 4; blk++) ka[blk] = kload(wave, blk);
+  float4 kc[4];
 #pragma unroll 1
   for (int kt = wave; kt < KT; kt += 8) {
 #pragma unroll
-    for (int blk = 0; blk < 4; blk++) kc[blk] = kload(kt + 4, blk);
-    qk_tile(ka, kt);
+    for (int blk = 0; blk < 4; blk++) kc[blk] = attn_kload(Kk, kr, wave, kt + 4, blk);
+    qk_tile(st.ka, kt);
     const int kn = kt + 8 < KT ? kt + 8 : kt;  // past the end: reloads, in bounds
 #pragma unroll
-    for (int blk = 0; blk < 4; blk++) ka[blk] = kload(kn, blk);
+    for (int blk = 0; blk < 4; blk++) st.ka[blk] = attn_kload(Kk, kr, wave, kn, blk);
     qk_tile(kc, kt + 4);
   }
-  __syncthreads();
+}
 
-  // ---- the chain on S, then P = softmax(S), by rows in place ------------------------
-  // The chain's ops (the same f32_binary, in order, per element) run here
-  // rather than after each product tile: a row's operands (a mask row) load
-  // as coalesced float4s, the next row's while this one is computed.
-  // Operand r of a lane's row holds element 4 (lane + 64 (r / 4)) + r % 4.
+// Phase two: the chain on S, then P = softmax(S), rows r0 .. r0 + nr - 1 in
+// place, one row at a time over the wave.  The chain's ops (the same
+// f32_binary, in order, per element) run here rather than after each product
+// tile: a row's operands (a mask row) load as coalesced float4s, the next
+// row's while this one is computed.  Operand r of a lane's row holds element
+// 4 (lane + 64 (r / 4)) + r % 4.
+template <int J, bool UNIT>
+__device__ __forceinline__ void attn_rows(const Epilogue &e1, float sm_sc, int64_t b, int64_t n0, float *S, int r0,
+                                          int nr) {
+  constexpr int NK = 256 * J, LS = NK + 4;
+  const int lane = threadIdx.x & 63;
   auto chain_off = [&](const EpiOp &o, int row, int r) {
     return b * o.s0 + (n0 + row) * o.s1 + (int64_t)(4 * (lane + kWave * (r / 4)) + r % 4) * o.s2;
   };
@@ -1381,17 +1498,17 @@ __global__ void __launch_bounds__(256, 2) attention_k(MfmaOperand Q, MfmaOperand
     }
   };
   float wn[kEpiEarly][4 * J];
-  chain_load(8 * wave, wn);
+  chain_load(r0, wn);
 #pragma unroll 1
-  for (int rr = 0; rr < kAttnRows / 4; rr++) {
-    const int ri = 8 * wave + rr;
+  for (int rr = 0; rr < nr; rr++) {
+    const int ri = r0 + rr;
     float *row = S + ri * LS;
     float wc[kEpiEarly][4 * J];
 #pragma unroll
     for (int k = 0; k < kEpiEarly; k++)
 #pragma unroll
       for (int r = 0; r < 4 * J; r++) wc[k][r] = wn[k][r];
-    if (rr + 1 < kAttnRows / 4) chain_load(ri + 1, wn);
+    if (rr + 1 < nr) chain_load(ri + 1, wn);
     float v[4 * J];
 #pragma unroll
     for (int j = 0; j < J; j++) {
@@ -1407,11 +1524,128 @@ __global__ void __launch_bounds__(256, 2) attention_k(MfmaOperand Q, MfmaOperand
 #pragma unroll
     for (int j = 0; j < J; j++) *reinterpret_cast<float4 *>(row + 4 * (lane + kWave * j)) = e[j];
   }
-  __syncthreads();
+}
 
-  // ---- O = P V: value columns 16 wave .., both query tiles -------------------------
-  const __amdgpu_buffer_rsrc_t vr =
-      __builtin_amdgcn_make_buffer_rsrc((void *)(V.p + boff(V, b)), (short)0, 0x7FFFFFFF, 0x00020000);
+// The first kEpiEarly chain ops inside the fused kernel.  Add, subtract,
+// multiply and divide run as the plain IEEE operation: only which operand's
+// NaN comes out can differ from f32_binary, never whether the result is NaN,
+// and a NaN anywhere in a row makes that softmax row, and so its rows of P
+// and O, NaN in the separate kernels and here alike.  Maximum and minimum
+// decide NaN-ness by their NaN rule, so they keep f32_binary.
+template <int NV>
+__device__ __forceinline__ void attn_chain_ops(const Epilogue &e, float (&v)[NV], const float (&w)[kEpiEarly][NV]) {
+#pragma unroll
+  for (int k = 0; k < kEpiEarly; k++) {
+    if (k >= e.n) break;
+    const EpiOp &o = e.op[k];
+    switch (o.code) {
+      case kAdd:
+#pragma unroll
+        for (int r = 0; r < NV; r++) v[r] = v[r] + w[k][r];
+        break;
+      case kMul:
+#pragma unroll
+        for (int r = 0; r < NV; r++) v[r] = v[r] * w[k][r];
+        break;
+      case kSub:
+        if (o.rev) {
+#pragma unroll
+          for (int r = 0; r < NV; r++) v[r] = w[k][r] - v[r];
+        } else {
+#pragma unroll
+          for (int r = 0; r < NV; r++) v[r] = v[r] - w[k][r];
+        }
+        break;
+      case kDiv:
+        if (o.rev) {
+#pragma unroll
+          for (int r = 0; r < NV; r++) v[r] = w[k][r] / v[r];
+        } else {
+#pragma unroll
+          for (int r = 0; r < NV; r++) v[r] = v[r] / w[k][r];
+        }
+        break;
+      case kMax: epi_op<kMax>(v, w[k], o.rev); break;
+      case kMin: epi_op<kMin>(v, w[k], o.rev); break;
+      default: break;
+    }
+  }
+}
+
+// Phase two for keys 256 and 512: rows r0 .. r0 + 7 as two passes of four
+// 16-lane rows (softmax_row16), the second pass's chain operands loaded while
+// the first pass's softmax runs.  Operand r of a lane's row holds element
+// 4 (i + 16 (r / 4)) + r % 4 (i = lane % 16); an operand constant along the
+// row (s2 = 0) is one load.
+template <int J, bool UNIT>
+__device__ __forceinline__ void attn_rows16(const Epilogue &e1, float sm_sc, int64_t b, int64_t n0, float *S,
+                                            int r0) {
+  constexpr int NK = 256 * J, LS = NK + 4, NJ = 4 * J, NV = 4 * NJ;
+  const int lane = threadIdx.x & 63, q = lane >> 4, li = lane & 15;
+  // The element stride goes through an empty asm: left visible, the
+  // compiler hoists all NV element offsets of the (rare) strided operands out
+  // of the pass loop and spills them.
+  auto chain_off = [&](const EpiOp &o, int row, int r) {
+    int64_t s2 = o.s2;
+    asm volatile("" : "+s"(s2));
+    return b * o.s0 + (n0 + row) * o.s1 + (int64_t)(4 * (li + 16 * (r / 4)) + r % 4) * s2;
+  };
+  auto chain_load = [&](int row, float (&w)[kEpiEarly][NV]) {
+#pragma unroll
+    for (int k = 0; k < kEpiEarly; k++) {
+      if (k >= e1.n) break;
+      const EpiOp &o = e1.op[k];
+      const float *p = o.p + b * o.s0 + (n0 + row) * o.s1;
+      if (o.s2 == 0) {
+        const float w0 = *p;
+#pragma unroll
+        for (int r = 0; r < NV; r++) w[k][r] = w0;
+      } else if (o.s2 == 1 && ((uintptr_t)p & 15) == 0) {
+#pragma unroll
+        for (int j = 0; j < NJ; j++) {
+          const float4 f = ld4(p + 4 * (li + 16 * j));
+          w[k][4 * j] = f.x, w[k][4 * j + 1] = f.y, w[k][4 * j + 2] = f.z, w[k][4 * j + 3] = f.w;
+        }
+      } else {
+#pragma unroll
+        for (int r = 0; r < NV; r++) w[k][r] = o.p[chain_off(o, row, r)];
+      }
+    }
+  };
+  float w[kEpiEarly][NV];
+  chain_load(r0 + q, w);
+#pragma unroll 1
+  for (int ps = 0; ps < 2; ps++) {
+    const int row = r0 + 4 * ps + q;
+    float *rp = S + row * LS;
+    float v[NV];
+#pragma unroll
+    for (int j = 0; j < NJ; j++) {
+      const float4 f = *reinterpret_cast<const float4 *>(rp + 4 * (li + 16 * j));
+      v[4 * j] = f.x, v[4 * j + 1] = f.y, v[4 * j + 2] = f.z, v[4 * j + 3] = f.w;
+    }
+    attn_chain_ops(e1, v, w);
+    if (ps == 0) chain_load(r0 + 4 + q, w);  // the second pass's operands load under this pass's softmax
+    epi_apply_n(e1, v, [&](const EpiOp &o, int r) { return chain_off(o, row, r); }, kEpiEarly);
+    float4 e[NJ];
+#pragma unroll
+    for (int j = 0; j < NJ; j++) e[j] = make_float4(v[4 * j], v[4 * j + 1], v[4 * j + 2], v[4 * j + 3]);
+    softmax_row16<NJ, UNIT>(e, sm_sc, rp);
+#pragma unroll
+    for (int j = 0; j < NJ; j++) *reinterpret_cast<float4 *>(rp + 4 * (li + 16 * j)) = e[j];
+  }
+}
+
+// Phase three: O = P V in ggml order, then the chain after it, stored.  V's
+// operands load four blocks ahead of their products, in two register sets
+// that take turns (NK / 16 is a multiple of 8): the loads of one set fly
+// while the other feeds the MFMAs, and no register moves between them.
+template <int J>
+__device__ __forceinline__ void attn_pv(const MfmaOperand &V, int64_t b, int64_t n0, int64_t NQ, int wave,
+                                        const float *S, const Epilogue &e2, float *__restrict__ O) {
+  constexpr int NK = 256 * J, LS = NK + 4, NB = NK / 16;
+  const int lane = threadIdx.x & 63, bl = lane >> 4, li = lane & 15;
+  const __amdgpu_buffer_rsrc_t vr = attn_rsrc(V, b);
   int vo[4];  // the lane's byte offsets of keys 4 bl + g, column 16 wave + li
 #pragma unroll
   for (int g = 0; g < 4; g++) vo[g] = (int)(((int64_t)(16 * wave + li) * V.sf + (int64_t)(4 * bl + g) * V.sk) * 4);
@@ -1426,10 +1660,6 @@ __global__ void __launch_bounds__(256, 2) attention_k(MfmaOperand Q, MfmaOperand
   auto pload = [&](int qt, int blk) {
     return *reinterpret_cast<const float4 *>(S + (16 * qt + li) * LS + 16 * blk + 4 * bl);
   };
-  // V's operands load four blocks ahead of their products, in two register
-  // sets that take turns (NK / 16 is a multiple of 8): the loads of one set
-  // fly while the other feeds the MFMAs, and no register moves between them.
-  constexpr int NB = NK / 16;
   v16f acc[2][4];
 #pragma unroll
   for (int qt = 0; qt < 2; qt++)
@@ -1465,6 +1695,31 @@ __global__ void __launch_bounds__(256, 2) attention_k(MfmaOperand Q, MfmaOperand
 #pragma unroll
     for (int r = 0; r < 4; r++) y[r * kAttnDv] = out[r];
   }
+}
+
+// One workgroup of four waves per block, the phases in turn.  Consecutive
+// query blocks of one batch share K and V: each XCD takes a contiguous run of
+// workgroups (whole batches), whose K and V stay in its L2.
+template <int J, bool UNIT>
+__global__ void __launch_bounds__(256, 2) attention_k(MfmaOperand Q, MfmaOperand Kk, MfmaOperand V, int64_t NQ,
+                                                      Epilogue e1, float sm_sc, Epilogue e2,
+                                                      float *__restrict__ O) {
+  constexpr int NK = 256 * J, LS = NK + 4;
+  __shared__ __attribute__((aligned(16))) float S[kAttnRows * LS];
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // an SGPR
+  uint32_t tx = blockIdx.x, ty = blockIdx.y;
+  if (gridDim.y > 1) xcd_tile(tx, ty);
+  const int64_t b = ty, n0 = (int64_t)tx * kAttnRows;
+  AttnQk st;
+  attn_qk_load(Q, Kk, b, n0, wave, st);
+  attn_qk<J>(Kk, b, wave, st, S);
+  __syncthreads();
+  if (J <= 2)
+    attn_rows16<J, UNIT>(e1, sm_sc, b, n0, S, 8 * wave);
+  else
+    attn_rows<J, UNIT>(e1, sm_sc, b, n0, S, 8 * wave, 8);
+  __syncthreads();
+  attn_pv<J>(V, b, n0, NQ, wave, S, e2, O);
 }
 
 // ---- rows longer than 4096 columns -------------------------------------------------
@@ -2308,16 +2563,19 @@ ArrayP attention_ggml(const DotOperand &q, const DotOperand &k, const DotOperand
   g_last_dot = strf("attention_k<%d>", J);
   launch([=](hipStream_t s) {
     (void)kq, (void)kk, (void)kvv, (void)keep;
-#define ATT_CASE(j)                                                                                  \
-  case j:                                                                                            \
-    if (unit) attention_k<j, true><<<grid, 256, 0, s>>>(Q, Kk, V, NQ, e1, sc, e2, Y);                \
-    else attention_k<j, false><<<grid, 256, 0, s>>>(Q, Kk, V, NQ, e1, sc, e2, Y);                    \
-    break;
-    switch (J) {
-      ATT_CASE(1) ATT_CASE(2) ATT_CASE(3) ATT_CASE(4)
-      default: break;
+    if (J == 1) {
+      if (unit) attention_k<1, true><<<grid, 256, 0, s>>>(Q, Kk, V, NQ, e1, sc, e2, Y);
+      else attention_k<1, false><<<grid, 256, 0, s>>>(Q, Kk, V, NQ, e1, sc, e2, Y);
+    } else if (J == 2) {
+      if (unit) attention_k<2, true><<<grid, 256, 0, s>>>(Q, Kk, V, NQ, e1, sc, e2, Y);
+      else attention_k<2, false><<<grid, 256, 0, s>>>(Q, Kk, V, NQ, e1, sc, e2, Y);
+    } else if (J == 3) {
+      if (unit) attention_k<3, true><<<grid, 256, 0, s>>>(Q, Kk, V, NQ, e1, sc, e2, Y);
+      else attention_k<3, false><<<grid, 256, 0, s>>>(Q, Kk, V, NQ, e1, sc, e2, Y);
+    } else if (J == 4) {
+      if (unit) attention_k<4, true><<<grid, 256, 0, s>>>(Q, Kk, V, NQ, e1, sc, e2, Y);
+      else attention_k<4, false><<<grid, 256, 0, s>>>(Q, Kk, V, NQ, e1, sc, e2, Y);
     }
-#undef ATT_CASE
   });
   return y;
 }

@@ -89,6 +89,10 @@ def bits_equal(a, b, nan_ok=False):
     return a.shape == b.shape and np.array_equal(na, nb) and np.array_equal(ua[~na], ub[~nb])
 
 
+def fused_name(NK):
+    return f"attention_k<{NK // 256}>"
+
+
 def run(text, ins, compile=True, faults=0):
     import shlo_hip
     m = shlo_hip.Module(text)
@@ -106,7 +110,24 @@ def test_fused_attention_vs_oracle(oracle, B, H, NQ, NK):
     for compile in (False, True):
         got = run(text, [q, k, v, mask], compile=compile)
         if not compile:
-            assert shlo_hip.last_dot_kernel() == f"attention_k<{NK // 256}>"
+            assert shlo_hip.last_dot_kernel() == fused_name(NK)
+        assert bits_equal(got, want), compile
+
+
+@pytest.mark.parametrize("B,H,NQ,NK", [(1, 29, 288, 256), (1, 13, 2528, 512), (2, 3, 1376, 256)])
+def test_fused_attention_runs(oracle, B, H, NQ, NK):
+    """More workgroups than two rounds over the CUs, grids not a multiple of
+    the XCD count (261, 1027 and 258 workgroups), long query runs."""
+    import shlo_hip
+    q, k, v = inputs(oracle, B, H, NQ, NK, seed=68)
+    i, j = np.arange(NQ)[:, None], np.arange(NK)[None, :]
+    mask = np.where(j > i % NK, F32(-np.inf), F32(0))  # causal, repeating: no row wholly masked
+    want = oracle_attn(oracle, q, k, v, mask)
+    text = attn_module(B, H, NQ, NK)
+    for compile in (False, True):
+        got = run(text, [q, k, v, mask], compile=compile)
+        if not compile:
+            assert shlo_hip.last_dot_kernel() == fused_name(NK)
         assert bits_equal(got, want), compile
 
 
@@ -136,7 +157,7 @@ def test_fused_attention_chain_variants(oracle, variant):
     for compile in (False, True):
         got = run(text, ins, compile=compile)
         if not compile:
-            assert shlo_hip.last_dot_kernel() == "attention_k<2>", variant
+            assert shlo_hip.last_dot_kernel() == fused_name(NK), variant
         assert bits_equal(got, want), (variant, compile)
 
 
@@ -161,7 +182,7 @@ def test_fused_attention_special_values(oracle):
     for compile in (False, True):
         got = run(text, [q, k, v, mask], compile=compile)
         if not compile:
-            assert shlo_hip.last_dot_kernel() == "attention_k<1>"
+            assert shlo_hip.last_dot_kernel() == fused_name(NK)
         assert bits_equal(got, want, nan_ok=True), compile
     assert np.isnan(want).any() and np.isfinite(want).any()
 
@@ -207,7 +228,7 @@ def test_fused_attention_head_views(oracle):
     for compile in (False, True):
         got = run(heads_module(B, T, H), [x], compile=compile)
         if not compile:
-            assert shlo_hip.last_dot_kernel() == "attention_k<1>"
+            assert shlo_hip.last_dot_kernel() == fused_name(T)
         assert bits_equal(got, want), compile
 
 
