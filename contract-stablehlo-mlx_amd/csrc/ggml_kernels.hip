@@ -1661,27 +1661,31 @@ __device__ __forceinline__ void attn_pv(const MfmaOperand &V, int64_t b, int64_t
     return *reinterpret_cast<const float4 *>(S + (16 * qt + li) * LS + 16 * blk + 4 * bl);
   };
   v16f acc[2][4];
-#pragma unroll
-  for (int qt = 0; qt < 2; qt++)
-#pragma unroll
-    for (int g = 0; g < 4; g++) acc[qt][g] = v16f{};
-  auto pv4 = [&](const float4 (&vs)[4], int blk0) {
+  // Block 0 starts the accumulators from the inline +0 (first); the loop
+  // from block 8 on.
+  auto pv4 = [&](const float4 (&vs)[4], int blk0, bool first) {
 #pragma unroll
     for (int i = 0; i < 4; i++)
 #pragma unroll
-      for (int qt = 0; qt < 2; qt++) mfma16_block(acc[qt], pload(qt, blk0 + i), vs[i], false);
+      for (int qt = 0; qt < 2; qt++) mfma16_block(acc[qt], pload(qt, blk0 + i), vs[i], first && i == 0);
   };
   float4 va[4], vb[4];
 #pragma unroll
   for (int i = 0; i < 4; i++) va[i] = vload(i);
+#pragma unroll
+  for (int i = 0; i < 4; i++) vb[i] = vload(4 + i);
+  pv4(va, 0, true);
+#pragma unroll
+  for (int i = 0; i < 4; i++) va[i] = vload(8 + i);
+  pv4(vb, 4, false);
 #pragma unroll 1
-  for (int b0 = 0; b0 < NB; b0 += 8) {
+  for (int b0 = 8; b0 < NB; b0 += 8) {
 #pragma unroll
     for (int i = 0; i < 4; i++) vb[i] = vload(b0 + 4 + i);
-    pv4(va, b0);
+    pv4(va, b0, false);
 #pragma unroll
     for (int i = 0; i < 4; i++) va[i] = vload(min(b0 + 8 + i, NB - 1));  // past the end: reloads, in bounds
-    pv4(vb, b0 + 4);
+    pv4(vb, b0 + 4, false);
   }
   const int64_t d = 16 * wave + li;
 #pragma unroll
@@ -1689,8 +1693,9 @@ __device__ __forceinline__ void attn_pv(const MfmaOperand &V, int64_t b, int64_t
     float out[4];
     tree16(acc[qt], out);
     const int64_t nq = n0 + 16 * qt + 4 * bl;
-    epi_apply_n(e2, out, [&](const EpiOp &o, int r) { return b * o.s0 + (nq + r) * o.s1 + d * o.s2; }, 0, NoUnary(),
-                DotUniform<true>());
+    if (e2.n > 0)
+      epi_apply_n(e2, out, [&](const EpiOp &o, int r) { return b * o.s0 + (nq + r) * o.s1 + d * o.s2; }, 0,
+                  NoUnary(), DotUniform<true>());
     float *y = O + (b * NQ + nq) * kAttnDv + d;
 #pragma unroll
     for (int r = 0; r < 4; r++) y[r * kAttnDv] = out[r];

@@ -258,3 +258,106 @@ def test_planted_faults_still_differ(oracle):
     for fault in ("dot_plain", "dot_builtin", "soft_max_float_sum", "binary_half", "broadcast_first"):
         got = run(text, [q, k, v, mask], faults=shlo_hip.fault_bits(fault))
         assert not bits_equal(got, want), fault
+
+
+@pytest.mark.parametrize("NK", [256, 512])
+def test_fused_attention_denominator_paths(oracle, NK):
+    """Scale 0 makes the chain's output the mask row itself (+-0 + m = m), so
+    the mask sets the softmax input exactly: rows whose denominator needs the
+    in-order walk (1/S within 2^-40 of a binary32 rounding boundary), rows
+    with entries 80-140 below the maximum (ggml_v_expf's subnormal branch and
+    its +0 branch), spread over both passes and all four 16-lane rows of a
+    wave, beside ordinary rows."""
+    import shlo_hip
+    from test_gpu_configs import _walk_rows
+    B, H, NQ = 1, 2, 64
+    q, k, v = inputs(oracle, B, H, NQ, NK, seed=69)
+    rng = np.random.default_rng(NK)
+    mask = rng.normal(0, 3, (NQ, NK)).astype(F32)
+    walk = _walk_rows(oracle, NK, 3)
+    for i, r in enumerate((0, 5, 10, 15, 36, 63)):
+        mask[r] = walk[i]
+    for r in (2, 7, 21, 40, 45):
+        mask[r] = rng.uniform(-140.0, -80.0, NK).astype(F32)
+        mask[r, r % NK] = 0.0
+        mask[r, -3:] = -np.inf
+    want = oracle_attn(oracle, q, k, v, mask, scale=0.0)
+    text = attn_module(B, H, NQ, NK, scale=0.0)
+    for compile in (False, True):
+        got = run(text, [q, k, v, mask], compile=compile)
+        if not compile:
+            assert shlo_hip.last_dot_kernel() == fused_name(NK)
+        assert bits_equal(got, want), compile
+
+
+def chain_module(B, H, NQ, NK, ops):
+    """QK^T, then `ops` in order: (op, operand, rev) with operand "c" (the
+    scalar constant 0.125 broadcast) or "m" (the [NQ, NK] argument broadcast
+    over batch and head); rev puts the running value second.  Then softmax, PV."""
+    q, k, v = t((B, H, NQ, 64)), t((B, H, NK, 64)), t((B, H, NK, 64))
+    s, o, m = t((B, H, NQ, NK)), t((B, H, NQ, 64)), t((NQ, NK))
+    qk = ("#stablehlo.dot<lhs_batching_dimensions = [0, 1], rhs_batching_dimensions = [0, 1], "
+          "lhs_contracting_dimensions = [3], rhs_contracting_dimensions = [3]>")
+    pv = ("#stablehlo.dot<lhs_batching_dimensions = [0, 1], rhs_batching_dimensions = [0, 1], "
+          "lhs_contracting_dimensions = [3], rhs_contracting_dimensions = [2]>")
+    L = [f'    %s0 = "stablehlo.dot_general"(%q, %k) {{dot_dimension_numbers = {qk}}} : ({q}, {k}) -> {s}',
+         f'    %c = "stablehlo.constant"() {{value = dense<0x3E000000> : tensor<f32>}} : () -> tensor<f32>',
+         f'    %cb = "stablehlo.broadcast_in_dim"(%c) {{broadcast_dimensions = array<i64>}} : (tensor<f32>) -> {s}',
+         f'    %mb = "stablehlo.broadcast_in_dim"(%mask) {{broadcast_dimensions = array<i64: 2, 3>}} : ({m}) -> {s}']
+    cur = "%s0"
+    for i, (op, operand, rev) in enumerate(ops):
+        w = "%cb" if operand == "c" else "%mb"
+        a, b = (w, cur) if rev else (cur, w)
+        L.append(f'    %s{i + 1} = "stablehlo.{op}"({a}, {b}) : ({s}, {s}) -> {s}')
+        cur = f"%s{i + 1}"
+    L += [f'    %p = "stablehlo.custom_call"({cur}) {{call_target_name = "ggml.soft_max", '
+          f'backend_config = "scale = 0x3F800000 : f32"}} : ({s}) -> {s}',
+          f'    %o = "stablehlo.dot_general"(%p, %v) {{dot_dimension_numbers = {pv}}} : ({s}, {v}) -> {o}']
+    body = "\n".join(L)
+    return (f"module {{\n  func.func public @main(%q: {q}, %k: {k}, %v: {v}, %mask: {m}) -> ({o}) {{\n"
+            f"{body}\n    func.return %o : {o}\n  }}\n}}\n")
+
+
+_NP = {"add": np.add, "subtract": np.subtract, "multiply": np.multiply, "divide": np.divide,
+       "maximum": np.maximum, "minimum": np.minimum}
+
+
+@pytest.mark.parametrize("ops", [
+    [("divide", "c", False), ("subtract", "m", True)],
+    [("subtract", "m", False), ("divide", "c", True)],
+    [("multiply", "c", True), ("maximum", "m", False)],
+    [("minimum", "m", True), ("add", "c", False)],
+    [("multiply", "c", False), ("add", "m", False), ("maximum", "m", True)],
+], ids=["div_rsub", "sub_rdiv", "rmul_max", "rmin_add", "three_ops"])
+def test_fused_attention_chain_ops(oracle, ops):
+    """Every chain op and operand order in the fused kernel, with NaN and inf
+    in Q (NaN scores: the row's P and O are NaN, compared by NaN-ness) and
+    +-inf and large finite mask entries; maximum and minimum decide NaN-ness by
+    their own rule.  The third op of three_ops runs after the two early ones."""
+    import shlo_hip
+    B, H, NQ, NK = 1, 2, 64, 256
+    q, k, v = inputs(oracle, B, H, NQ, NK, seed=70)
+    q[0, 0, 3, 7] = np.nan
+    q[0, 1, 9, :] *= F32(1e30)  # inf * finite scores
+    rng = np.random.default_rng(71)
+    mask = rng.normal(0, 2, (NQ, NK)).astype(F32)
+    mask[5, 10] = np.nan
+    mask[6, :100] = -np.inf
+    mask[7, 3] = np.inf
+    mask[8, 1::2] = F32(3e38)
+    s = oracle.dot_general_bnk(q.reshape(B * H, NQ, 64), k.reshape(B * H, NK, 64))
+    with np.errstate(all="ignore"):
+        for op, operand, rev in ops:
+            w = np.broadcast_to(F32(0.125), s.shape) if operand == "c" else np.broadcast_to(mask[None], s.shape)
+            a, b = (w, s) if rev else (s, w)
+            s = _NP[op](a, b).astype(F32)
+        p = oracle.soft_max(s)
+    vt = np.ascontiguousarray(v.reshape(B * H, NK, 64).transpose(0, 2, 1))
+    want = oracle.dot_general_bnk(p, vt).reshape(B, H, NQ, 64)
+    text = chain_module(B, H, NQ, NK, ops)
+    for compile in (False, True):
+        got = run(text, [q, k, v, mask], compile=compile)
+        if not compile:
+            assert shlo_hip.last_dot_kernel() == fused_name(NK)
+        assert bits_equal(got, want, nan_ok=True), compile
+    assert np.isnan(want).any() and np.isfinite(want).any()

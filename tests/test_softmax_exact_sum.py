@@ -242,3 +242,60 @@ def test_interval_and_walk_paths():
         assert inv == inv_of(chain(parts)), path
         paths[path] = paths.get(path, 0) + 1
     assert paths.get("exact", 0) > 100 and paths.get("interval", 0) > 100, paths
+
+
+def row16_sums(parts):
+    """The fused attention kernel's order for rows of 16 n groups on 16 lanes:
+    lane i sums the parts g = i + 16 j in ascending j, then the row's DPP
+    grouping (row16_sum's four steps) over the 16 lane sums."""
+    ls = np.zeros(16)
+    for g, p in enumerate(np.asarray(parts, np.float32)):
+        ls[g % 16] = ls[g % 16] + np.float64(p)
+    i = np.arange(16)
+    for src in (i ^ 1, i ^ 2, (i & 8) | (7 - (i & 7)), 15 - i):
+        ls = ls + ls[src]
+    assert np.all(ls == ls[0])
+    return ls[0]
+
+
+def kernel_inv16(parts):
+    parts = np.asarray(parts, np.float32)
+    le = int(part_ulp_exp(parts).min()) if len(parts) else 255
+    t = row16_sums(parts)
+    if t <= limit(le):
+        assert np.float64(t).view(np.uint64) == np.float64(chain(parts)).view(np.uint64)
+        return inv_of(t), "exact"
+    d = t * 2.0 ** -40
+    lo, hi = inv_of(t + d), inv_of(t - d)
+    if lo == hi:
+        return lo, "interval"
+    return inv_of(walk(parts)[0]), "walk"
+
+
+def test_sixteen_lane_rows():
+    """The 16-lane order (rows of 256 and 512 columns in the fused attention
+    kernel): a row that passes has tree == chain, and every path's inv is
+    (float)(1.0 / in-order sum), over random, softmax-like and walk rows."""
+    rng = np.random.default_rng(11)
+    paths = {}
+    for _ in range(1200):
+        n = int(rng.choice([64, 128]))
+        parts = random_parts(rng, n, float(rng.uniform(0, 120)))
+        inv, path = kernel_inv16(parts)
+        assert inv == inv_of(chain(parts)), path
+        paths[path] = paths.get(path, 0) + 1
+    for _ in range(200):
+        x = rng.normal(0, 4, 512).astype(np.float32)
+        e = np.exp(x - x.max()).astype(np.float32).reshape(128, 4)
+        parts = ((e[:, 0] + e[:, 1]) + (e[:, 2] + e[:, 3])).astype(np.float32)
+        inv, path = kernel_inv16(parts)
+        assert inv == inv_of(chain(parts)), path
+        paths[path] = paths.get(path, 0) + 1
+    tiny = np.float32(2.0 ** -100)
+    for n in (64, 128):
+        for P in near_boundary(0.0, 10):
+            parts = np.concatenate([[P], np.full(n - 1, tiny, np.float32)]).astype(np.float32)
+            inv, path = kernel_inv16(parts)
+            assert inv == inv_of(chain(parts)) and path == "walk", (P, path)
+            paths[path] = paths.get(path, 0) + 1
+    assert all(paths.get(k, 0) > 15 for k in ("exact", "interval", "walk")), paths
