@@ -1305,9 +1305,18 @@ __device__ __forceinline__ void softmax_row16(float4 (&e)[NJ], float sc, float *
     mx = __builtin_fmaxf(mx, __builtin_fmaxf(__builtin_fmaxf(e[j].x, e[j].y), __builtin_fmaxf(e[j].z, e[j].w)));
   }
   mx = row16_max_f(mx);
+  // A slice j that holds only -inf on every lane, with each row's maximum
+  // neither -inf nor NaN, gives ggml_v_expf(-inf - mx) = +0 throughout (its
+  // |n| > 192 branch): it is set, not computed (a causal mask's upper half).
+  const bool mx_ok = mx > -__builtin_inff();
   bool mid = false;
 #pragma unroll
   for (int j = 0; j < NJ; j++) {
+    const float ninf = -__builtin_inff();
+    if (__all(mx_ok && e[j].x == ninf && e[j].y == ninf && e[j].z == ninf && e[j].w == ninf)) {
+      e[j] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      continue;
+    }
     bool m0, m1, m2, m3;
     e[j].x = ggml_v_expf_nonpos(e[j].x - mx, &m0);
     e[j].y = ggml_v_expf_nonpos(e[j].y - mx, &m1);

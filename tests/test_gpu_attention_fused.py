@@ -361,3 +361,33 @@ def test_fused_attention_chain_ops(oracle, ops):
             assert shlo_hip.last_dot_kernel() == fused_name(NK)
         assert bits_equal(got, want, nan_ok=True), compile
     assert np.isnan(want).any() and np.isfinite(want).any()
+
+
+@pytest.mark.parametrize("sm_scale", [1.0, 0.5, -1.0])
+def test_fused_attention_masked_slices(oracle, sm_scale):
+    """A 64-column slice that is -inf on all four rows of a pass is set to
+    +0 without computing it; the rows here check where that must not happen:
+    a wholly -inf row (its maximum is -inf: NaN throughout), a NaN inside
+    an otherwise -inf slice (the row is NaN), +inf among -inf, and a negative
+    softmax scale (which turns -inf into +inf).  Scale 0 makes the mask row
+    the softmax input; NaN outputs compare by NaN-ness."""
+    import shlo_hip
+    B, H, NQ, NK = 1, 2, 32, 512
+    q, k, v = inputs(oracle, B, H, NQ, NK, seed=72)
+    rng = np.random.default_rng(73)
+    mask = rng.normal(0, 3, (NQ, NK)).astype(F32)
+    mask[:, 128:] = -np.inf           # slices 2 .. 7 masked on every row
+    mask[3, :] = -np.inf              # a wholly masked row
+    mask[9, 300] = np.nan             # NaN in a masked slice
+    mask[18, 450] = np.inf            # +inf in a masked slice
+    mask[27, 64:128] = -np.inf        # one more masked slice on one row only
+    want = oracle_attn(oracle, q, k, v, mask, scale=0.0, sm_scale=sm_scale)
+    text = attn_module(B, H, NQ, NK, scale=0.0, sm_scale=sm_scale)
+    for compile in (False, True):
+        got = run(text, [q, k, v, mask], compile=compile)
+        if not compile:
+            assert shlo_hip.last_dot_kernel() == fused_name(NK)
+        assert bits_equal(got, want, nan_ok=True), compile
+    assert np.isnan(want[0, :, 3]).all() and np.isnan(want[0, :, 9]).all()
+    # a negative scale turns the masked -inf into +inf: every row is NaN
+    assert np.isfinite(want[0, :, 0]).all() == (sm_scale > 0)
