@@ -391,3 +391,42 @@ def test_fused_attention_masked_slices(oracle, sm_scale):
     assert np.isnan(want[0, :, 3]).all() and np.isnan(want[0, :, 9]).all()
     # a negative scale turns the masked -inf into +inf: every row is NaN
     assert np.isfinite(want[0, :, 0]).all() == (sm_scale > 0)
+
+
+def test_fused_attention_zero_slice_after_negative_zero(oracle):
+    """Zero products still count: a chain at -0 plus a +0 product is +0, so
+    P V cannot drop a slice whose P is +0 on every row while an accumulator
+    holds -0 (any such shortcut must check for it).  Row 5 here
+    has P = 2^-149 on keys 0..15 (V = -0.25 there: each chain's first
+    product underflows to -0), P = 1 on key 16 (V = -0), then zeros with
+    negative V (the chains stay -0) and, in the masked last slice, zeros with
+    positive V: ggml's chains end at +0, so O[5] is +0, where dropping the
+    slice would leave -0.  Scale 0 makes the mask row the softmax input."""
+    import shlo_hip
+    B, H, NQ, NK = 1, 1, 32, 256
+    q, k, _ = inputs(oracle, B, H, NQ, NK, seed=74)
+    rng = np.random.default_rng(75)
+    mask = rng.normal(0, 1, (NQ, NK)).astype(F32)
+    mask[:, 192:] = -np.inf
+    # x with ggml_v_expf(x) = 2^-149, the smallest subnormal
+    lo, hi = np.float32(-104.0), np.float32(-103.0)
+    tiny = np.float32(2.0 ** -149)
+    xs = np.sort(np.arange(np.float32(hi).view(np.int32), np.float32(lo).view(np.int32) + 1, dtype=np.int32).view(np.float32))
+    hits = [x for x in xs if oracle.ggml_v_expf(np.float32(x)) == tiny]
+    assert hits
+    mask[5, :] = -np.inf
+    mask[5, :16] = hits[len(hits) // 2]
+    mask[5, 16] = 0.0
+    v = np.empty((B, H, NK, 64), F32)
+    v[..., :16, :] = -0.25
+    v[..., 16, :] = -0.0
+    v[..., 17:192, :] = -rng.uniform(0.5, 1.5, (B, H, 175, 64)).astype(F32)
+    v[..., 192:, :] = rng.uniform(0.5, 1.5, (B, H, 64, 64)).astype(F32)
+    want = oracle_attn(oracle, q, k, v, mask, scale=0.0)
+    assert np.all(want[0, 0, 5].view(np.uint32) == 0)  # +0 in ggml's order
+    text = attn_module(B, H, NQ, NK, scale=0.0)
+    for compile in (False, True):
+        got = run(text, [q, k, v, mask], compile=compile)
+        if not compile:
+            assert shlo_hip.last_dot_kernel() == fused_name(NK)
+        assert bits_equal(got, want), compile
