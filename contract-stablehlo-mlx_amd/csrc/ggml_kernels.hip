@@ -1437,16 +1437,140 @@ __device__ __forceinline__ void attn_qk_load(const MfmaOperand &Q, const MfmaOpe
   for (int blk = 0; blk < 4; blk++) st.ka[blk] = attn_kload(Kk, kr, wave, wave, blk);
 }
 
+// The largest exponent field (bits 23..30) among a wave's values, the same
+// on every lane.
+__device__ __forceinline__ int wave_max_expfield(int v) {
+  v = max(v, dpp_i<kDppXor1>(v));
+  v = max(v, dpp_i<kDppXor2>(v));
+  v = max(v, dpp_i<kDppHalfMirror>(v));
+  v = max(v, dpp_i<kDppMirror>(v));
+  v = max(max(__builtin_amdgcn_readlane(v, 0), __builtin_amdgcn_readlane(v, 16)),
+          max(__builtin_amdgcn_readlane(v, 32), __builtin_amdgcn_readlane(v, 48)));
+  return v >> 23;
+}
+__device__ __forceinline__ int expfield4(const float4 &x, int v) {
+  v = max(v, (int)(f_bits(x.x) & 0x7F800000u));
+  v = max(v, (int)(f_bits(x.y) & 0x7F800000u));
+  v = max(v, (int)(f_bits(x.z) & 0x7F800000u));
+  return max(v, (int)(f_bits(x.w) & 0x7F800000u));
+}
+
+// Masked key tiles (mskip = 1: the chain is one add of a row operand, the
+// mask, shared by every batch; mskip = 2: a multiply by one scalar c, then
+// that add).  attn_prep_k finds the masked tiles and K's largest exponents
+// in a launch of its own before the kernel.  A key tile of
+// 16 keys whose mask is -inf on all 32 rows of the block needs no products
+// when Q, K (and c) are finite and small enough that no partial sum of a
+// score can overflow: then every score S is finite, S c is finite, and the
+// chain gives S (c) + -inf = -inf whatever S is, the same as from S = 0, which
+// is written instead.  With |q| < 2^(eq+1) and |k| < 2^(ek+1) (exponents of
+// the largest magnitudes) every partial sum of the 64 products, rounding
+// included, stays below 2^(eq+ek+9), so eq + ek + 9 <= 127, or
+// eq + ek + ec + 10 <= 127 with the multiply, keeps everything finite.
+struct AttnSkip {
+  uint32_t bits;  // bit i: the wave's tile w + 4 i is skipped
+};
+
+template <int J>
+__device__ __forceinline__ AttnSkip attn_skip_plan(const Epilogue &e1, int mskip, const int *__restrict__ prep,
+                                                   int64_t b, int64_t n0, int64_t NQ, int64_t B, int wave,
+                                                   const AttnQk &st) {
+  constexpr int NK = 256 * J, KT = NK / 16, NC = NK / 64;
+  AttnSkip sk;
+  sk.bits = 0;
+  if (!mskip) return sk;
+  // attn_prep_k's output: K's exponent fields per (batch, 64 keys), then per
+  // (block of 32 rows, 64 keys) the masked-tile bits of its four key tiles.
+  // Tile w + 4 i is tile w of chunk i.
+  const int *mb = prep + B * NC + (n0 / kAttnRows) * NC;
+#pragma unroll
+  for (int i = 0; i < KT / 4; i++) sk.bits |= (uint32_t)((mb[i] >> wave) & 1) << i;
+  int q = 0;
+#pragma unroll
+  for (int qt = 0; qt < 2; qt++)
+#pragma unroll
+    for (int blk = 0; blk < 4; blk++) q = expfield4(st.qa[qt][blk], q);
+  const int qf = wave_max_expfield(q);
+  const int cf = mskip == 2 ? (int)((f_bits(e1.op[0].p[0]) >> 23) & 0xFF) : 0;
+  int kf = 0;
+#pragma unroll
+  for (int c = 0; c < NC; c++) kf = max(kf, prep[b * NC + c]);
+  // inf or NaN anywhere in Q, K or c (field 255), or a bound too large:
+  // compute every tile
+  if (qf == 255 || cf == 255 || kf == 255 || qf + kf + cf > (mskip == 2 ? 498 : 372)) sk.bits = 0;
+  return sk;
+}
+
+// attn_skip_plan's inputs, one launch of B NC + (NQ / 32) NC workgroups
+// (NC = NK / 64): the first B NC take the largest exponent field of K per
+// (batch, 64 keys); the rest take a block of 32 mask rows (the mask is shared
+// by every batch: s0 = 0) by 64 keys and set bit t of their int when the
+// block's key tile 4 c + t is -inf on all 32 rows.  K rows and mask rows are
+// 16-byte aligned (the host checks).
+__global__ void __launch_bounds__(256) attn_prep_k(MfmaOperand Kk, int NK, int64_t B, const float *__restrict__ mask,
+                                                   int64_t ms1, int *__restrict__ out) {
+  __shared__ int part[4];
+  const int NC = NK / 64;
+  const int64_t wg = blockIdx.x;
+  int v = 0;
+  if (wg < B * NC) {
+    const int64_t bb = wg / NC, c = wg % NC;
+    const float *kb = Kk.p + boff(Kk, bb) + 64 * c * Kk.sf;
+#pragma unroll
+    for (int i = 0; i < 4; i++) {  // 64 keys x 16 float4s, four per thread
+      const int g = threadIdx.x + 256 * i;
+      v = expfield4(ld4(kb + (int64_t)(g >> 4) * Kk.sf + 4 * (g & 15)), v);
+    }
+    v = wave_max_expfield(v) << 23;
+  } else {
+    // 32 rows x 16 float4s: two per thread, rows t / 16 and t / 16 + 16, key
+    // quad t % 16 (tile (t % 16) / 4); the bits of tiles with an entry that
+    // is not -inf, ORed over the workgroup
+    const int64_t blk = (wg - B * NC) / NC, c = (wg - B * NC) % NC;
+    const float *m = mask + (blk * kAttnRows + (threadIdx.x >> 4)) * ms1 + 64 * c + 4 * (threadIdx.x & 15);
+    const float ninf = -__builtin_inff();
+    const float4 x = ld4(m), y = ld4(m + 16 * ms1);
+    const bool all = x.x == ninf && x.y == ninf && x.z == ninf && x.w == ninf && y.x == ninf && y.y == ninf &&
+                     y.z == ninf && y.w == ninf;
+    v = all ? 0 : 1 << ((threadIdx.x & 15) >> 2);
+    v |= dpp_i<kDppXor1>(v);
+    v |= dpp_i<kDppXor2>(v);
+    v |= dpp_i<kDppHalfMirror>(v);
+    v |= dpp_i<kDppMirror>(v);
+    v = (__builtin_amdgcn_readlane(v, 0) | __builtin_amdgcn_readlane(v, 16)) |
+        (__builtin_amdgcn_readlane(v, 32) | __builtin_amdgcn_readlane(v, 48));
+  }
+  if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = v;
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    if (wg < B * NC)
+      out[wg] = max(max(part[0], part[1]), max(part[2], part[3])) >> 23;
+    else
+      out[wg] = ~(part[0] | part[1] | part[2] | part[3]) & 15;
+  }
+}
+
 // Phase one: S = Q K^T in ggml order.  Key tiles in two register sets that
 // take turns (a wave's KT / 4 tiles are an even count): one set's loads fly
 // while the other's products run.
 template <int J>
-__device__ __forceinline__ void attn_qk(const MfmaOperand &Kk, int64_t b, int wave, AttnQk &st, float *S) {
+__device__ __forceinline__ void attn_qk(const MfmaOperand &Kk, int64_t b, int wave, AttnQk &st, float *S,
+                                        const AttnSkip &sk) {
   constexpr int NK = 256 * J, KT = NK / 16, LS = NK + 4;
   const int lane = threadIdx.x & 63, bl = lane >> 4, li = lane & 15;
   const __amdgpu_buffer_rsrc_t kr = attn_rsrc(Kk, b);
+  // A skipped tile (masked on every row, the bound holding) loads nothing
+  // and stores S = 0.
+  auto skipped = [&](int kt) { return ((sk.bits >> ((kt - wave) >> 2)) & 1u) != 0; };
   auto qk_tile = [&](const float4 (&ks)[4], int kt) {
     const int m = 16 * kt + li;
+    if (skipped(kt)) {
+#pragma unroll
+      for (int qt = 0; qt < 2; qt++)
+#pragma unroll
+        for (int r = 0; r < 4; r++) S[(16 * qt + 4 * bl + r) * LS + m] = 0.0f;
+      return;
+    }
 #pragma unroll
     for (int qt = 0; qt < 2; qt++) {
       v16f acc[4];
@@ -1461,12 +1585,16 @@ __device__ __forceinline__ void attn_qk(const MfmaOperand &Kk, int64_t b, int wa
   float4 kc[4];
 #pragma unroll 1
   for (int kt = wave; kt < KT; kt += 8) {
+    if (!skipped(kt + 4)) {
 #pragma unroll
-    for (int blk = 0; blk < 4; blk++) kc[blk] = attn_kload(Kk, kr, wave, kt + 4, blk);
+      for (int blk = 0; blk < 4; blk++) kc[blk] = attn_kload(Kk, kr, wave, kt + 4, blk);
+    }
     qk_tile(st.ka, kt);
     const int kn = kt + 8 < KT ? kt + 8 : kt;  // past the end: reloads, in bounds
+    if (!skipped(kn)) {
 #pragma unroll
-    for (int blk = 0; blk < 4; blk++) st.ka[blk] = attn_kload(Kk, kr, wave, kn, blk);
+      for (int blk = 0; blk < 4; blk++) st.ka[blk] = attn_kload(Kk, kr, wave, kn, blk);
+    }
     qk_tile(kc, kt + 4);
   }
 }
@@ -1716,17 +1844,29 @@ __device__ __forceinline__ void attn_pv(const MfmaOperand &V, int64_t b, int64_t
 // workgroups (whole batches), whose K and V stay in its L2.
 template <int J, bool UNIT>
 __global__ void __launch_bounds__(256, 2) attention_k(MfmaOperand Q, MfmaOperand Kk, MfmaOperand V, int64_t NQ,
-                                                      Epilogue e1, float sm_sc, Epilogue e2,
-                                                      float *__restrict__ O) {
+                                                      Epilogue e1, int mskip, const int *__restrict__ prep,
+                                                      float sm_sc, Epilogue e2, float *__restrict__ O) {
   constexpr int NK = 256 * J, LS = NK + 4;
   __shared__ __attribute__((aligned(16))) float S[kAttnRows * LS];
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // an SGPR
   uint32_t tx = blockIdx.x, ty = blockIdx.y;
-  if (gridDim.y > 1) xcd_tile(tx, ty);
+  if (mskip) {
+    // Masked tiles make blocks unequal (a causal mask leaves the first query
+    // blocks the least work): the heaviest blocks of every batch go first, so
+    // the lighter ones fill in behind them.  Consecutive ids walk the
+    // batches, so XCD x (ids x mod 8) keeps batches x mod 8 when B is a
+    // multiple of 8.
+    const uint32_t lin = blockIdx.x + gridDim.x * blockIdx.y;
+    ty = lin % gridDim.y;
+    tx = gridDim.x - 1 - lin / gridDim.y;
+  } else if (gridDim.y > 1) {
+    xcd_tile(tx, ty);
+  }
   const int64_t b = ty, n0 = (int64_t)tx * kAttnRows;
   AttnQk st;
   attn_qk_load(Q, Kk, b, n0, wave, st);
-  attn_qk<J>(Kk, b, wave, st, S);
+  const AttnSkip sk = attn_skip_plan<J>(e1, mskip, prep, b, n0, NQ, gridDim.y, wave, st);
+  attn_qk<J>(Kk, b, wave, st, S, sk);
   __syncthreads();
   if (J <= 2)
     attn_rows16<J, UNIT>(e1, sm_sc, b, n0, S, 8 * wave);
@@ -2564,6 +2704,19 @@ ArrayP attention_ggml(const DotOperand &q, const DotOperand &k, const DotOperand
       if (o.code == kEpiGeluErf) return nullptr;
   std::vector<ArrayP> keep;
   const Epilogue e1 = make_epilogue(epi1, &keep), e2 = make_epilogue(epi2, &keep);
+  // Masked-tile skipping (attn_skip_plan): the chain is [add mask] or
+  // [multiply by a scalar, add mask], the mask along keys with 16-byte
+  // aligned rows.
+  int mskip = 0;
+  {
+    auto mask_ok = [](const EpiOp &o) {
+      return o.code == kAdd && o.s0 == 0 && o.s2 == 1 && (uintptr_t)o.p % 16 == 0 && o.s1 % 4 == 0;
+    };
+    if (e1.n == 1 && mask_ok(e1.op[0])) mskip = 1;
+    if (e1.n == 2 && e1.op[0].code == kMul && e1.op[0].s0 == 0 && e1.op[0].s1 == 0 && e1.op[0].s2 == 0 &&
+        mask_ok(e1.op[1]))
+      mskip = 2;
+  }
   auto y = new_array(kF32, Shape{B * NQ * DV});
   const MfmaOperand Q{(const float *)q.arr->data(), q.sb, q.sf, q.sk, NQ, q.sb2, q.nb2};
   const MfmaOperand Kk{(const float *)k.arr->data(), k.sb, k.sf, k.sk, NK, k.sb2, k.nb2};
@@ -2574,21 +2727,30 @@ ArrayP attention_ggml(const DotOperand &q, const DotOperand &k, const DotOperand
   const dim3 grid((unsigned)(NQ / kAttnRows), (unsigned)B);
   const int J = (int)(NK / 256);
   ArrayP kq = q.arr, kk = k.arr, kvv = v.arr;
+  // attn_prep_k's ints: K's exponent fields per (batch, 64 keys), then the
+  // masked-tile bits per (block of 32 query rows, 64 keys)
+  const int64_t nprep = (B + NQ / kAttnRows) * (NK / 64);
+  ArrayP kxa = mskip ? new_array(kF32, Shape{nprep}) : nullptr;
+  int *kx = kxa ? (int *)kxa->data() : nullptr;
+  const float *mp = mskip ? e1.op[mskip - 1].p : nullptr;
+  const int64_t ms1 = mskip ? e1.op[mskip - 1].s1 : 0;
   g_last_dot = strf("attention_k<%d>", J);
   launch([=](hipStream_t s) {
-    (void)kq, (void)kk, (void)kvv, (void)keep;
+    (void)kq, (void)kk, (void)kvv, (void)keep, (void)kxa;
+    if (mskip)
+      attn_prep_k<<<(unsigned)nprep, 256, 0, s>>>(Kk, (int)NK, B, mp, ms1, kx);
     if (J == 1) {
-      if (unit) attention_k<1, true><<<grid, 256, 0, s>>>(Q, Kk, V, NQ, e1, sc, e2, Y);
-      else attention_k<1, false><<<grid, 256, 0, s>>>(Q, Kk, V, NQ, e1, sc, e2, Y);
+      if (unit) attention_k<1, true><<<grid, 256, 0, s>>>(Q, Kk, V, NQ, e1, mskip, kx, sc, e2, Y);
+      else attention_k<1, false><<<grid, 256, 0, s>>>(Q, Kk, V, NQ, e1, mskip, kx, sc, e2, Y);
     } else if (J == 2) {
-      if (unit) attention_k<2, true><<<grid, 256, 0, s>>>(Q, Kk, V, NQ, e1, sc, e2, Y);
-      else attention_k<2, false><<<grid, 256, 0, s>>>(Q, Kk, V, NQ, e1, sc, e2, Y);
+      if (unit) attention_k<2, true><<<grid, 256, 0, s>>>(Q, Kk, V, NQ, e1, mskip, kx, sc, e2, Y);
+      else attention_k<2, false><<<grid, 256, 0, s>>>(Q, Kk, V, NQ, e1, mskip, kx, sc, e2, Y);
     } else if (J == 3) {
-      if (unit) attention_k<3, true><<<grid, 256, 0, s>>>(Q, Kk, V, NQ, e1, sc, e2, Y);
-      else attention_k<3, false><<<grid, 256, 0, s>>>(Q, Kk, V, NQ, e1, sc, e2, Y);
+      if (unit) attention_k<3, true><<<grid, 256, 0, s>>>(Q, Kk, V, NQ, e1, mskip, kx, sc, e2, Y);
+      else attention_k<3, false><<<grid, 256, 0, s>>>(Q, Kk, V, NQ, e1, mskip, kx, sc, e2, Y);
     } else if (J == 4) {
-      if (unit) attention_k<4, true><<<grid, 256, 0, s>>>(Q, Kk, V, NQ, e1, sc, e2, Y);
-      else attention_k<4, false><<<grid, 256, 0, s>>>(Q, Kk, V, NQ, e1, sc, e2, Y);
+      if (unit) attention_k<4, true><<<grid, 256, 0, s>>>(Q, Kk, V, NQ, e1, mskip, kx, sc, e2, Y);
+      else attention_k<4, false><<<grid, 256, 0, s>>>(Q, Kk, V, NQ, e1, mskip, kx, sc, e2, Y);
     }
   });
   return y;

@@ -430,3 +430,49 @@ def test_fused_attention_zero_slice_after_negative_zero(oracle):
         if not compile:
             assert shlo_hip.last_dot_kernel() == fused_name(NK)
         assert bits_equal(got, want), compile
+
+
+@pytest.mark.parametrize("NK", [256, 512])
+@pytest.mark.parametrize("case", ["plain", "k_huge_masked", "k_nan_masked", "q_inf", "near_limit", "over_limit",
+                                  "scale_inf", "mask_only"])
+def test_fused_attention_masked_tiles(oracle, NK, case):
+    """Key tiles whose mask is -inf on all 32 rows of a block skip their
+    products when Q, K and the scale bound every score and its scaled value
+    below overflow (then the chain gives -inf whatever the score is).  Here
+    the bound holds, or fails by a hair, or fails through inf, NaN or
+    overflowing scores that sit only in masked tiles (they turn whole rows
+    NaN); NaN outputs compare by NaN-ness."""
+    import shlo_hip
+    B, H, NQ = 1, 2, 64
+    q, k, v = inputs(oracle, B, H, NQ, NK, seed=76)
+    scale, mask_arg = 0.125, True
+    if case == "k_huge_masked":
+        k[0, 0, 200, :] = F32(3e38)      # masked for every query row: scores overflow there
+        k[0, 1, 100, ::2] = F32(-3e38)
+    elif case == "k_nan_masked":
+        k[0, 1, 150, 7] = np.nan
+    elif case == "q_inf":
+        q[0, 0, 40, 3] = np.inf
+    elif case == "near_limit":  # |q|, |k| < 2^60 with c = 2^-3: eq + ek + ec + 10 = 126
+        q = (np.sign(q) * F32(2.0 ** 59)).astype(F32)
+        k = (np.sign(k) * F32(2.0 ** 59)).astype(F32)
+    elif case == "over_limit":  # 2^62: the bound fails and the scores overflow to +-inf
+        q = (np.sign(q) * F32(2.0 ** 62)).astype(F32)
+        k = (np.sign(k) * F32(2.0 ** 62)).astype(F32)
+    elif case == "scale_inf":
+        scale = float("inf")
+    elif case == "mask_only":
+        scale = None
+    mask = causal(NQ, NK)
+    with np.errstate(all="ignore"):  # the overflowing cases overflow in the oracle too
+        want = oracle_attn(oracle, q, k, v, mask, scale=scale)
+    text = attn_module(B, H, NQ, NK, scale=scale)
+    for compile in (False, True):
+        got = run(text, [q, k, v, mask], compile=compile)
+        if not compile:
+            assert shlo_hip.last_dot_kernel() == fused_name(NK)
+        assert bits_equal(got, want, nan_ok=True), (case, compile)
+    if case in ("plain", "near_limit", "mask_only"):
+        assert np.isfinite(want).all()
+    if case in ("k_nan_masked", "q_inf", "over_limit", "scale_inf"):
+        assert np.isnan(want).any()
