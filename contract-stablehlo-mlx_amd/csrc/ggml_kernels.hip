@@ -1347,9 +1347,12 @@ __device__ __forceinline__ void softmax_row16(float4 (&e)[NJ], float sc, float *
 //
 // One workgroup per (batch, 32 query rows): S and then P stay in LDS, so the
 // score matrix never goes through HBM.  Every value is the one the separate
-// kernels give: S in ggml_vec_dot_f32 order then the fused chain (the same
-// f32_binary), each row through softmax_row (the soft_max kernel's code), and
-// O in ggml order again.
+// kernels give: S in ggml_vec_dot_f32 order, then the fused chain (the same
+// IEEE operations; attn_chain_ops says where a NaN's payload may differ),
+// each row through softmax_row16 or softmax_row (the soft_max kernel's
+// decisions), and O in ggml order again.  Work whose result is fixed without
+// it is skipped: softmax slices that are -inf on every row, and key tiles
+// that a mask sets to -inf on all 32 rows (attn_skip_plan).
 //
 // The products run on v_mfma_f32_16x16x1_4b_f32 (K = 1: one fused
 // multiply-add per output per instruction, as the 32x32 form): lane l
