@@ -1294,8 +1294,12 @@ __device__ __forceinline__ float ordered_sum16(const float (&part)[NJ], Fin fin)
 // row's values e also stored at rp (4 (i + 16 j) for group j): the rare
 // recomputation of the 126 < |n| <= 192 exponentials reads them back rather
 // than keeping the arguments in registers.
+//
+// Returns (the same in every lane) bit j set when slice j of all four rows
+// came out +0 exactly: the slice was set to zeros and every row's reciprocal
+// is finite (a NaN reciprocal, from a NaN in the row, makes the slice NaN).
 template <int NJ, bool UNIT>
-__device__ __forceinline__ void softmax_row16(float4 (&e)[NJ], float sc, float *rp) {
+__device__ __forceinline__ uint32_t softmax_row16(float4 (&e)[NJ], float sc, float *rp) {
   const int li = threadIdx.x & 15;
   float mx = -__builtin_inff();
 #pragma unroll
@@ -1310,11 +1314,16 @@ __device__ __forceinline__ void softmax_row16(float4 (&e)[NJ], float sc, float *
   // |n| > 192 branch): it is set, not computed (a causal mask's upper half).
   const bool mx_ok = mx > -__builtin_inff();
   bool mid = false;
+  uint32_t zero = 0;
 #pragma unroll
   for (int j = 0; j < NJ; j++) {
-    const float ninf = -__builtin_inff();
-    if (__all(mx_ok && e[j].x == ninf && e[j].y == ninf && e[j].z == ninf && e[j].w == ninf)) {
+    // maximum (IEEE 754-2019: a NaN operand gives NaN) of the four is -inf
+    // exactly when all four are -inf: two v_maximum3_f32 and one compare
+    const float m4 = __builtin_elementwise_maximum(__builtin_elementwise_maximum(e[j].x, e[j].y),
+                                                   __builtin_elementwise_maximum(e[j].z, e[j].w));
+    if (__all(mx_ok && m4 == -__builtin_inff())) {
       e[j] = make_float4(0.0f, 0.0f, 0.0f, 0.0f);
+      zero |= 1u << j;
       continue;
     }
     bool m0, m1, m2, m3;
@@ -1341,6 +1350,7 @@ __device__ __forceinline__ void softmax_row16(float4 (&e)[NJ], float sc, float *
   const float inv = ordered_sum16<NJ>(part, [](double x) { return (float)(1.0 / x); });
 #pragma unroll
   for (int j = 0; j < NJ; j++) e[j] = make_float4(e[j].x * inv, e[j].y * inv, e[j].z * inv, e[j].w * inv);
+  return __all(__builtin_isfinite(inv)) ? zero : 0u;
 }
 
 // ---- fused attention: S = Q K^T, its element-wise chain, ggml.soft_max, O = P V ----------
@@ -1472,6 +1482,7 @@ __device__ __forceinline__ int expfield4(const float4 &x, int v) {
 // eq + ek + ec + 10 <= 127 with the multiply, keeps everything finite.
 struct AttnSkip {
   uint32_t bits;  // bit i: the wave's tile w + 4 i is skipped
+  uint32_t vbad;  // bit c: V may hold an infinite or NaN value among keys 64 c .. 64 c + 63
 };
 
 template <int J>
@@ -1481,6 +1492,7 @@ __device__ __forceinline__ AttnSkip attn_skip_plan(const Epilogue &e1, int mskip
   constexpr int NK = 256 * J, KT = NK / 16, NC = NK / 64;
   AttnSkip sk;
   sk.bits = 0;
+  sk.vbad = ~0u;
   if (!mskip) return sk;
   // attn_prep_k's output: K's exponent fields per (batch, 64 keys), then per
   // (block of 32 rows, 64 keys) the masked-tile bits of its four key tiles.
@@ -1496,8 +1508,13 @@ __device__ __forceinline__ AttnSkip attn_skip_plan(const Epilogue &e1, int mskip
   const int qf = wave_max_expfield(q);
   const int cf = mskip == 2 ? (int)((f_bits(e1.op[0].p[0]) >> 23) & 0xFF) : 0;
   int kf = 0;
+  sk.vbad = 0;
 #pragma unroll
-  for (int c = 0; c < NC; c++) kf = max(kf, prep[b * NC + c]);
+  for (int c = 0; c < NC; c++) {
+    const int pk = prep[b * NC + c];
+    kf = max(kf, pk & 0xFF);
+    sk.vbad |= (uint32_t)((pk >> 8) & 1) << c;
+  }
   // inf or NaN anywhere in Q, K or c (field 255), or a bound too large:
   // compute every tile
   if (qf == 255 || cf == 255 || kf == 255 || qf + kf + cf > (mskip == 2 ? 498 : 372)) sk.bits = 0;
@@ -1506,25 +1523,41 @@ __device__ __forceinline__ AttnSkip attn_skip_plan(const Epilogue &e1, int mskip
 
 // attn_skip_plan's inputs, one launch of B NC + (NQ / 32) NC workgroups
 // (NC = NK / 64): the first B NC take the largest exponent field of K per
-// (batch, 64 keys); the rest take a block of 32 mask rows (the mask is shared
-// by every batch: s0 = 0) by 64 keys and set bit t of their int when the
+// (batch, 64 keys), with bit 8 set when V has an infinite or NaN value among
+// those keys; the rest take a block of 32 mask rows (the mask is shared by
+// every batch: s0 = 0) by 64 keys and set bit t of their int when the
 // block's key tile 4 c + t is -inf on all 32 rows.  K rows and mask rows are
 // 16-byte aligned (the host checks).
-__global__ void __launch_bounds__(256) attn_prep_k(MfmaOperand Kk, int NK, int64_t B, const float *__restrict__ mask,
-                                                   int64_t ms1, int *__restrict__ out) {
-  __shared__ int part[4];
+__global__ void __launch_bounds__(256) attn_prep_k(MfmaOperand Kk, MfmaOperand V, int NK, int64_t B,
+                                                   const float *__restrict__ mask, int64_t ms1, int *__restrict__ out) {
+  __shared__ int part[4], vpart[4];
   const int NC = NK / 64;
   const int64_t wg = blockIdx.x;
   int v = 0;
   if (wg < B * NC) {
     const int64_t bb = wg / NC, c = wg % NC;
     const float *kb = Kk.p + boff(Kk, bb) + 64 * c * Kk.sf;
+    const float *vb = V.p + boff(V, bb) + 64 * c * V.sk;
+    float4 kv[4];
+    float vv[16];
 #pragma unroll
     for (int i = 0; i < 4; i++) {  // 64 keys x 16 float4s, four per thread
       const int g = threadIdx.x + 256 * i;
-      v = expfield4(ld4(kb + (int64_t)(g >> 4) * Kk.sf + 4 * (g & 15)), v);
+      kv[i] = ld4(kb + (int64_t)(g >> 4) * Kk.sf + 4 * (g & 15));
     }
+#pragma unroll
+    for (int i = 0; i < 16; i++) {  // 64 keys x 64 values (unit stride along values), 16 per thread
+      const int g = threadIdx.x + 256 * i;
+      vv[i] = vb[(int64_t)(g >> 6) * V.sk + (g & 63)];
+    }
+#pragma unroll
+    for (int i = 0; i < 4; i++) v = expfield4(kv[i], v);
     v = wave_max_expfield(v) << 23;
+    int w = 0;
+#pragma unroll
+    for (int i = 0; i < 4; i++) w = expfield4(make_float4(vv[4 * i], vv[4 * i + 1], vv[4 * i + 2], vv[4 * i + 3]), w);
+    w = wave_max_expfield(w);
+    if ((threadIdx.x & 63) == 0) vpart[threadIdx.x >> 6] = w;
   } else {
     // 32 rows x 16 float4s: two per thread, rows t / 16 and t / 16 + 16, key
     // quad t % 16 (tile (t % 16) / 4); the bits of tiles with an entry that
@@ -1546,25 +1579,29 @@ __global__ void __launch_bounds__(256) attn_prep_k(MfmaOperand Kk, int NK, int64
   if ((threadIdx.x & 63) == 0) part[threadIdx.x >> 6] = v;
   __syncthreads();
   if (threadIdx.x == 0) {
-    if (wg < B * NC)
-      out[wg] = max(max(part[0], part[1]), max(part[2], part[3])) >> 23;
-    else
+    if (wg < B * NC) {
+      const int vf = max(max(vpart[0], vpart[1]), max(vpart[2], vpart[3]));
+      out[wg] = (max(max(part[0], part[1]), max(part[2], part[3])) >> 23) | (vf == 255 ? 0x100 : 0);
+    } else {
       out[wg] = ~(part[0] | part[1] | part[2] | part[3]) & 15;
+    }
   }
 }
 
 // Phase one: S = Q K^T in ggml order.  Key tiles in two register sets that
 // take turns (a wave's KT / 4 tiles are an even count): one set's loads fly
 // while the other's products run.
-template <int J>
+template <int J, bool SKIP>
 __device__ __forceinline__ void attn_qk(const MfmaOperand &Kk, int64_t b, int wave, AttnQk &st, float *S,
                                         const AttnSkip &sk) {
   constexpr int NK = 256 * J, KT = NK / 16, LS = NK + 4;
   const int lane = threadIdx.x & 63, bl = lane >> 4, li = lane & 15;
   const __amdgpu_buffer_rsrc_t kr = attn_rsrc(Kk, b);
   // A skipped tile (masked on every row, the bound holding) loads nothing
-  // and stores S = 0.
-  auto skipped = [&](int kt) { return ((sk.bits >> ((kt - wave) >> 2)) & 1u) != 0; };
+  // and stores S = 0.  Without skipping (SKIP false) every load is
+  // unconditional, so the wait before a tile's products counts the next
+  // tile's loads as still in flight rather than waiting for them.
+  auto skipped = [&](int kt) { return SKIP && ((sk.bits >> ((kt - wave) >> 2)) & 1u) != 0; };
   auto qk_tile = [&](const float4 (&ks)[4], int kt) {
     const int m = 16 * kt + li;
     if (skipped(kt)) {
@@ -1672,42 +1709,57 @@ __device__ __forceinline__ void attn_rows(const Epilogue &e1, float sm_sc, int64
 // and a NaN anywhere in a row makes that softmax row, and so its rows of P
 // and O, NaN in the separate kernels and here alike.  Maximum and minimum
 // decide NaN-ness by their NaN rule, so they keep f32_binary.
+// w[k] holds op k's operand for each element of the lane's row, or, when it
+// is one value along the row (s2 = 0), wu[k] holds that value.
 template <int NV>
-__device__ __forceinline__ void attn_chain_ops(const Epilogue &e, float (&v)[NV], const float (&w)[kEpiEarly][NV]) {
+__device__ __forceinline__ void attn_chain_op(const EpiOp &o, float (&v)[NV], const float (&w)[NV]) {
+  switch (o.code) {
+    case kAdd:
+#pragma unroll
+      for (int r = 0; r < NV; r++) v[r] = v[r] + w[r];
+      break;
+    case kMul:
+#pragma unroll
+      for (int r = 0; r < NV; r++) v[r] = v[r] * w[r];
+      break;
+    case kSub:
+      if (o.rev) {
+#pragma unroll
+        for (int r = 0; r < NV; r++) v[r] = w[r] - v[r];
+      } else {
+#pragma unroll
+        for (int r = 0; r < NV; r++) v[r] = v[r] - w[r];
+      }
+      break;
+    case kDiv:
+      if (o.rev) {
+#pragma unroll
+        for (int r = 0; r < NV; r++) v[r] = w[r] / v[r];
+      } else {
+#pragma unroll
+        for (int r = 0; r < NV; r++) v[r] = v[r] / w[r];
+      }
+      break;
+    case kMax: epi_op<kMax>(v, w, o.rev); break;
+    case kMin: epi_op<kMin>(v, w, o.rev); break;
+    default: break;
+  }
+}
+
+template <int NV>
+__device__ __forceinline__ void attn_chain_ops(const Epilogue &e, float (&v)[NV], const float (&w)[kEpiEarly][NV],
+                                               const float (&wu)[kEpiEarly]) {
 #pragma unroll
   for (int k = 0; k < kEpiEarly; k++) {
     if (k >= e.n) break;
     const EpiOp &o = e.op[k];
-    switch (o.code) {
-      case kAdd:
+    if (o.s2 == 0) {
+      float t[NV];
 #pragma unroll
-        for (int r = 0; r < NV; r++) v[r] = v[r] + w[k][r];
-        break;
-      case kMul:
-#pragma unroll
-        for (int r = 0; r < NV; r++) v[r] = v[r] * w[k][r];
-        break;
-      case kSub:
-        if (o.rev) {
-#pragma unroll
-          for (int r = 0; r < NV; r++) v[r] = w[k][r] - v[r];
-        } else {
-#pragma unroll
-          for (int r = 0; r < NV; r++) v[r] = v[r] - w[k][r];
-        }
-        break;
-      case kDiv:
-        if (o.rev) {
-#pragma unroll
-          for (int r = 0; r < NV; r++) v[r] = w[k][r] / v[r];
-        } else {
-#pragma unroll
-          for (int r = 0; r < NV; r++) v[r] = v[r] / w[k][r];
-        }
-        break;
-      case kMax: epi_op<kMax>(v, w[k], o.rev); break;
-      case kMin: epi_op<kMin>(v, w[k], o.rev); break;
-      default: break;
+      for (int r = 0; r < NV; r++) t[r] = wu[k];
+      attn_chain_op(o, v, t);
+    } else {
+      attn_chain_op(o, v, w[k]);
     }
   }
 }
@@ -1716,10 +1768,11 @@ __device__ __forceinline__ void attn_chain_ops(const Epilogue &e, float (&v)[NV]
 // 16-lane rows (softmax_row16), the second pass's chain operands loaded while
 // the first pass's softmax runs.  Operand r of a lane's row holds element
 // 4 (i + 16 (r / 4)) + r % 4 (i = lane % 16); an operand constant along the
-// row (s2 = 0) is one load.
+// row (s2 = 0) is one load.  Returns the 64-key slices whose P is +0 on all
+// eight rows (bit j: keys 64 j .. 64 j + 63).
 template <int J, bool UNIT>
-__device__ __forceinline__ void attn_rows16(const Epilogue &e1, float sm_sc, int64_t b, int64_t n0, float *S,
-                                            int r0) {
+__device__ __forceinline__ uint32_t attn_rows16(const Epilogue &e1, float sm_sc, int64_t b, int64_t n0, float *S,
+                                                int r0) {
   constexpr int NK = 256 * J, LS = NK + 4, NJ = 4 * J, NV = 4 * NJ;
   const int lane = threadIdx.x & 63, q = lane >> 4, li = lane & 15;
   // The element stride goes through an empty asm: left visible, the
@@ -1730,16 +1783,14 @@ __device__ __forceinline__ void attn_rows16(const Epilogue &e1, float sm_sc, int
     asm volatile("" : "+s"(s2));
     return b * o.s0 + (n0 + row) * o.s1 + (int64_t)(4 * (li + 16 * (r / 4)) + r % 4) * s2;
   };
-  auto chain_load = [&](int row, float (&w)[kEpiEarly][NV]) {
+  auto chain_load = [&](int row, float (&w)[kEpiEarly][NV], float (&wu)[kEpiEarly]) {
 #pragma unroll
     for (int k = 0; k < kEpiEarly; k++) {
       if (k >= e1.n) break;
       const EpiOp &o = e1.op[k];
       const float *p = o.p + b * o.s0 + (n0 + row) * o.s1;
       if (o.s2 == 0) {
-        const float w0 = *p;
-#pragma unroll
-        for (int r = 0; r < NV; r++) w[k][r] = w0;
+        wu[k] = *p;
       } else if (o.s2 == 1 && ((uintptr_t)p & 15) == 0) {
 #pragma unroll
         for (int j = 0; j < NJ; j++) {
@@ -1752,10 +1803,9 @@ __device__ __forceinline__ void attn_rows16(const Epilogue &e1, float sm_sc, int
       }
     }
   };
-  float w[kEpiEarly][NV];
-  chain_load(r0 + q, w);
-#pragma unroll 1
-  for (int ps = 0; ps < 2; ps++) {
+  float wa[kEpiEarly][NV], wb[kEpiEarly][NV], wua[kEpiEarly], wub[kEpiEarly];
+  auto pass = [&](int ps, const float (&w)[kEpiEarly][NV], const float (&wu)[kEpiEarly])
+                  __attribute__((always_inline)) {
     const int row = r0 + 4 * ps + q;
     float *rp = S + row * LS;
     float v[NV];
@@ -1764,25 +1814,38 @@ __device__ __forceinline__ void attn_rows16(const Epilogue &e1, float sm_sc, int
       const float4 f = *reinterpret_cast<const float4 *>(rp + 4 * (li + 16 * j));
       v[4 * j] = f.x, v[4 * j + 1] = f.y, v[4 * j + 2] = f.z, v[4 * j + 3] = f.w;
     }
-    attn_chain_ops(e1, v, w);
-    if (ps == 0) chain_load(r0 + 4 + q, w);  // the second pass's operands load under this pass's softmax
+    attn_chain_ops(e1, v, w, wu);
+    if (ps == 0) chain_load(r0 + 4 + q, wb, wub);  // the second pass's operands load under this pass's softmax
     epi_apply_n(e1, v, [&](const EpiOp &o, int r) { return chain_off(o, row, r); }, kEpiEarly);
     float4 e[NJ];
 #pragma unroll
     for (int j = 0; j < NJ; j++) e[j] = make_float4(v[4 * j], v[4 * j + 1], v[4 * j + 2], v[4 * j + 3]);
-    softmax_row16<NJ, UNIT>(e, sm_sc, rp);
+    const uint32_t zero = softmax_row16<NJ, UNIT>(e, sm_sc, rp);
 #pragma unroll
     for (int j = 0; j < NJ; j++) *reinterpret_cast<float4 *>(rp + 4 * (li + 16 * j)) = e[j];
-  }
+    return zero;
+  };
+  // Each pass has its own operand registers and both passes are inlined, so
+  // the second pass's operands need no copy between the passes.
+  chain_load(r0 + q, wa, wua);
+  const uint32_t z0 = pass(0, wa, wua);
+  return z0 & pass(1, wb, wub);
 }
 
 // Phase three: O = P V in ggml order, then the chain after it, stored.  V's
 // operands load four blocks ahead of their products, in two register sets
-// that take turns (NK / 16 is a multiple of 8): the loads of one set fly
-// while the other feeds the MFMAs, and no register moves between them.
+// that take turns: the loads of one set fly while the other feeds the MFMAs,
+// and no register moves between them.
+//
+// The products run over the first nzb blocks of 16 keys (a multiple of 4,
+// at least 4).  The blocks after them have P = +0 on all 32 rows (a causal
+// mask's upper part) and finite V (the caller checks both): each of their
+// products adds +0 * v = +-0 to a chain, which leaves the chain's value
+// unchanged, bit for bit, unless the chain is -0 (-0 + +0 = +0).  If any of
+// the wave's chains is -0 the remaining products run as well, in order.
 template <int J>
 __device__ __forceinline__ void attn_pv(const MfmaOperand &V, int64_t b, int64_t n0, int64_t NQ, int wave,
-                                        const float *S, const Epilogue &e2, float *__restrict__ O) {
+                                        const float *S, int nzb, const Epilogue &e2, float *__restrict__ O) {
   constexpr int NK = 256 * J, LS = NK + 4, NB = NK / 16;
   const int lane = threadIdx.x & 63, bl = lane >> 4, li = lane & 15;
   const __amdgpu_buffer_rsrc_t vr = attn_rsrc(V, b);
@@ -1801,31 +1864,85 @@ __device__ __forceinline__ void attn_pv(const MfmaOperand &V, int64_t b, int64_t
     return *reinterpret_cast<const float4 *>(S + (16 * qt + li) * LS + 16 * blk + 4 * bl);
   };
   v16f acc[2][4];
-  // Block 0 starts the accumulators from the inline +0 (first); the loop
-  // from block 8 on.
-  auto pv4 = [&](const float4 (&vs)[4], int blk0, bool first) {
+  if constexpr (J >= 2) {
+    // Block 0 starts the accumulators from the inline +0 (first).
+    auto pv4 = [&](const float4 (&vs)[4], const float4 (&ps)[4][2], bool first) {
 #pragma unroll
-    for (int i = 0; i < 4; i++)
+      for (int i = 0; i < 4; i++)
 #pragma unroll
-      for (int qt = 0; qt < 2; qt++) mfma16_block(acc[qt], pload(qt, blk0 + i), vs[i], first && i == 0);
-  };
-  float4 va[4], vb[4];
+        for (int qt = 0; qt < 2; qt++) mfma16_block(acc[qt], ps[i][qt], vs[i], first && i == 0);
+    };
+    auto pl4 = [&](float4 (&ps)[4][2], int blk0) {
 #pragma unroll
-  for (int i = 0; i < 4; i++) va[i] = vload(i);
+      for (int i = 0; i < 4; i++)
 #pragma unroll
-  for (int i = 0; i < 4; i++) vb[i] = vload(4 + i);
-  pv4(va, 0, true);
+        for (int qt = 0; qt < 2; qt++) ps[i][qt] = pload(qt, min(blk0 + i, nzb - 1));
+    };
+    float4 va[4], vb[4], pa[4][2], pb[4][2];
 #pragma unroll
-  for (int i = 0; i < 4; i++) va[i] = vload(8 + i);
-  pv4(vb, 4, false);
+    for (int i = 0; i < 4; i++) va[i] = vload(i);
+#pragma unroll
+    for (int i = 0; i < 4; i++) vb[i] = vload(min(4 + i, nzb - 1));  // past nzb: reloads, in bounds
+    pl4(pa, 0);
+    pl4(pb, 4);
+    pv4(va, pa, true);
 #pragma unroll 1
-  for (int b0 = 8; b0 < NB; b0 += 8) {
+    for (int b0 = 4; b0 < nzb; b0 += 8) {  // vb, pb hold blocks b0 .. b0 + 3
 #pragma unroll
-    for (int i = 0; i < 4; i++) vb[i] = vload(b0 + 4 + i);
-    pv4(va, b0, false);
+      for (int i = 0; i < 4; i++) va[i] = vload(min(b0 + 4 + i, nzb - 1));
+      pl4(pa, b0 + 4);
+      __builtin_amdgcn_sched_barrier(0);
+      pv4(vb, pb, false);
+      __builtin_amdgcn_sched_barrier(0);
+      if (b0 + 4 >= nzb) break;
 #pragma unroll
-    for (int i = 0; i < 4; i++) va[i] = vload(min(b0 + 8 + i, NB - 1));  // past the end: reloads, in bounds
-    pv4(vb, b0 + 4, false);
+      for (int i = 0; i < 4; i++) vb[i] = vload(min(b0 + 8 + i, nzb - 1));
+      pl4(pb, b0 + 8);
+      __builtin_amdgcn_sched_barrier(0);
+      pv4(va, pa, false);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  } else {
+    // Block 0 starts the accumulators from the inline +0 (first).
+    auto pv4 = [&](const float4 (&vs)[4], int blk0, bool first) {
+#pragma unroll
+      for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int qt = 0; qt < 2; qt++) mfma16_block(acc[qt], pload(qt, blk0 + i), vs[i], first && i == 0);
+    };
+    float4 va[4], vb[4];
+#pragma unroll
+    for (int i = 0; i < 4; i++) va[i] = vload(i);
+#pragma unroll
+    for (int i = 0; i < 4; i++) vb[i] = vload(min(4 + i, nzb - 1));  // past nzb: reloads, in bounds
+    pv4(va, 0, true);
+#pragma unroll 1
+    for (int b0 = 4; b0 < nzb; b0 += 8) {  // vb holds blocks b0 .. b0 + 3
+#pragma unroll
+      for (int i = 0; i < 4; i++) va[i] = vload(min(b0 + 4 + i, nzb - 1));
+      pv4(vb, b0, false);
+      if (b0 + 4 >= nzb) break;
+#pragma unroll
+      for (int i = 0; i < 4; i++) vb[i] = vload(min(b0 + 8 + i, nzb - 1));
+      pv4(va, b0 + 4, false);
+    }
+  }
+  if (nzb < NB) {
+    bool neg0 = false;
+#pragma unroll
+    for (int qt = 0; qt < 2; qt++)
+#pragma unroll
+      for (int i = 0; i < 4; i++)
+#pragma unroll
+        for (int r = 0; r < 16; r++) neg0 |= __builtin_amdgcn_classf(acc[qt][i][r], 32);  // -0
+    if (__any(neg0)) {
+#pragma unroll 1
+      for (int blk = nzb; blk < NB; blk++) {
+        const float4 v = vload(blk);
+#pragma unroll
+        for (int qt = 0; qt < 2; qt++) mfma16_block(acc[qt], pload(qt, blk), v, false);
+      }
+    }
   }
   const int64_t d = 16 * wave + li;
 #pragma unroll
@@ -1845,23 +1962,32 @@ __device__ __forceinline__ void attn_pv(const MfmaOperand &V, int64_t b, int64_t
 // One workgroup of four waves per block, the phases in turn.  Consecutive
 // query blocks of one batch share K and V: each XCD takes a contiguous run of
 // workgroups (whole batches), whose K and V stay in its L2.
-template <int J, bool UNIT>
+template <int J, bool UNIT, bool SKIP>
 __global__ void __launch_bounds__(256, 2) attention_k(MfmaOperand Q, MfmaOperand Kk, MfmaOperand V, int64_t NQ,
                                                       Epilogue e1, int mskip, const int *__restrict__ prep,
                                                       float sm_sc, Epilogue e2, float *__restrict__ O) {
   constexpr int NK = 256 * J, LS = NK + 4;
   __shared__ __attribute__((aligned(16))) float S[kAttnRows * LS];
+  __shared__ uint32_t zs[4];
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // an SGPR
   uint32_t tx = blockIdx.x, ty = blockIdx.y;
-  if (mskip) {
+  if (SKIP) {
     // Masked tiles make blocks unequal (a causal mask leaves the first query
-    // blocks the least work): the heaviest blocks of every batch go first, so
-    // the lighter ones fill in behind them.  Consecutive ids walk the
-    // batches, so XCD x (ids x mod 8) keeps batches x mod 8 when B is a
-    // multiple of 8.
+    // blocks the least work).  Blocks are ranked h = 0 (heaviest: the last
+    // query block of every batch) .. nb - 1, and dispatched so that the two
+    // workgroups a CU starts with are a heavy and a light one: ids 0 .. 255
+    // (one per CU of the 256) take the heaviest ranks, ids 256 .. 511 (each
+    // CU's second) the lightest, the rest the middle ranks, heaviest first.
+    // A heavy block's waves wait on their own dependences as much as they
+    // issue, and a light block fills those gaps, where two light blocks
+    // together would leave the CU mostly idle.  Consecutive ranks walk the
+    // batches.
     const uint32_t lin = blockIdx.x + gridDim.x * blockIdx.y;
-    ty = lin % gridDim.y;
-    tx = gridDim.x - 1 - lin / gridDim.y;
+    const uint32_t nb = gridDim.x * gridDim.y, C = 256;
+    uint32_t h = lin;
+    if (nb >= 2 * C) h = lin < C ? lin : lin < 2 * C ? nb - 1 - (lin - C) : lin - C;
+    ty = h % gridDim.y;
+    tx = gridDim.x - 1 - h / gridDim.y;
   } else if (gridDim.y > 1) {
     xcd_tile(tx, ty);
   }
@@ -1869,14 +1995,21 @@ __global__ void __launch_bounds__(256, 2) attention_k(MfmaOperand Q, MfmaOperand
   AttnQk st;
   attn_qk_load(Q, Kk, b, n0, wave, st);
   const AttnSkip sk = attn_skip_plan<J>(e1, mskip, prep, b, n0, NQ, gridDim.y, wave, st);
-  attn_qk<J>(Kk, b, wave, st, S, sk);
+  attn_qk<J, SKIP>(Kk, b, wave, st, S, sk);
   __syncthreads();
+  uint32_t zero = 0;  // 64-key slices whose P is +0 on this wave's rows
   if (J <= 2)
-    attn_rows16<J, UNIT>(e1, sm_sc, b, n0, S, 8 * wave);
+    zero = attn_rows16<J, UNIT>(e1, sm_sc, b, n0, S, 8 * wave);
   else
     attn_rows<J, UNIT>(e1, sm_sc, b, n0, S, 8 * wave, 8);
+  if ((threadIdx.x & 63) == 0) zs[wave] = zero;
   __syncthreads();
-  attn_pv<J>(V, b, n0, NQ, wave, S, e2, O);
+  // Products run up to the last slice with a nonzero P on any of the 32 rows,
+  // when V is finite on the slices after it (else over all keys).
+  const uint32_t live = ~(zs[0] & zs[1] & zs[2] & zs[3]) & ((1u << (NK / 64)) - 1);
+  int nzb = live ? 4 * (32 - __builtin_clz(live)) : 4;
+  if (sk.vbad >> (nzb / 4)) nzb = NK / 16;
+  attn_pv<J>(V, b, n0, NQ, wave, S, nzb, e2, O);
 }
 
 // ---- rows longer than 4096 columns -------------------------------------------------
@@ -2685,6 +2818,23 @@ ArrayP dot_ggml(const DotOperand &lhs, const DotOperand &rhs, int64_t B, int64_t
   return y;
 }
 
+
+// One attention_k launch: the instance for J keys / 256, a unit softmax
+// scale or not, masked-tile skipping or not (a no-op unless `on`).
+template <int J>
+void attention_launch(bool on, bool unit, bool skip, dim3 grid, hipStream_t s, const MfmaOperand &Q,
+                      const MfmaOperand &Kk, const MfmaOperand &V, int64_t NQ, const Epilogue &e1, int mskip,
+                      const int *prep, float sc, const Epilogue &e2, float *Y) {
+  if (!on) return;
+  if (skip) {
+    if (unit) attention_k<J, true, true><<<grid, 256, 0, s>>>(Q, Kk, V, NQ, e1, mskip, prep, sc, e2, Y);
+    else attention_k<J, false, true><<<grid, 256, 0, s>>>(Q, Kk, V, NQ, e1, mskip, prep, sc, e2, Y);
+  } else {
+    if (unit) attention_k<J, true, false><<<grid, 256, 0, s>>>(Q, Kk, V, NQ, e1, mskip, prep, sc, e2, Y);
+    else attention_k<J, false, false><<<grid, 256, 0, s>>>(Q, Kk, V, NQ, e1, mskip, prep, sc, e2, Y);
+  }
+}
+
 ArrayP attention_ggml(const DotOperand &q, const DotOperand &k, const DotOperand &v, int64_t B, int64_t NQ,
                       int64_t NK, int64_t DH, int64_t DV, const std::vector<FusedOp> &epi1, uint32_t sm_scale_bits,
                       const std::vector<FusedOp> &epi2) {
@@ -2741,20 +2891,11 @@ ArrayP attention_ggml(const DotOperand &q, const DotOperand &k, const DotOperand
   launch([=](hipStream_t s) {
     (void)kq, (void)kk, (void)kvv, (void)keep, (void)kxa;
     if (mskip)
-      attn_prep_k<<<(unsigned)nprep, 256, 0, s>>>(Kk, (int)NK, B, mp, ms1, kx);
-    if (J == 1) {
-      if (unit) attention_k<1, true><<<grid, 256, 0, s>>>(Q, Kk, V, NQ, e1, mskip, kx, sc, e2, Y);
-      else attention_k<1, false><<<grid, 256, 0, s>>>(Q, Kk, V, NQ, e1, mskip, kx, sc, e2, Y);
-    } else if (J == 2) {
-      if (unit) attention_k<2, true><<<grid, 256, 0, s>>>(Q, Kk, V, NQ, e1, mskip, kx, sc, e2, Y);
-      else attention_k<2, false><<<grid, 256, 0, s>>>(Q, Kk, V, NQ, e1, mskip, kx, sc, e2, Y);
-    } else if (J == 3) {
-      if (unit) attention_k<3, true><<<grid, 256, 0, s>>>(Q, Kk, V, NQ, e1, mskip, kx, sc, e2, Y);
-      else attention_k<3, false><<<grid, 256, 0, s>>>(Q, Kk, V, NQ, e1, mskip, kx, sc, e2, Y);
-    } else if (J == 4) {
-      if (unit) attention_k<4, true><<<grid, 256, 0, s>>>(Q, Kk, V, NQ, e1, mskip, kx, sc, e2, Y);
-      else attention_k<4, false><<<grid, 256, 0, s>>>(Q, Kk, V, NQ, e1, mskip, kx, sc, e2, Y);
-    }
+      attn_prep_k<<<(unsigned)nprep, 256, 0, s>>>(Kk, V, (int)NK, B, mp, ms1, kx);
+    attention_launch<1>(J == 1, unit, mskip != 0, grid, s, Q, Kk, V, NQ, e1, mskip, kx, sc, e2, Y);
+    attention_launch<2>(J == 2, unit, mskip != 0, grid, s, Q, Kk, V, NQ, e1, mskip, kx, sc, e2, Y);
+    attention_launch<3>(J == 3, unit, mskip != 0, grid, s, Q, Kk, V, NQ, e1, mskip, kx, sc, e2, Y);
+    attention_launch<4>(J == 4, unit, mskip != 0, grid, s, Q, Kk, V, NQ, e1, mskip, kx, sc, e2, Y);
   });
   return y;
 }

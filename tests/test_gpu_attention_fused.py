@@ -433,6 +433,53 @@ def test_fused_attention_zero_slice_after_negative_zero(oracle):
 
 
 @pytest.mark.parametrize("NK", [256, 512])
+@pytest.mark.parametrize("case", ["plain", "v_inf", "v_nan", "neg_zero"])
+def test_fused_attention_pv_zero_suffix(oracle, NK, case):
+    """Under a square causal mask each block of 32 query rows has P = +0 on
+    all its rows from some 64-key slice on, and P V leaves those products out
+    when the wave's value columns are finite there and no chain is at -0.
+    Here they are, or a masked value is +-inf or NaN (0 * inf is NaN: those
+    columns turn NaN), or every chain is at -0 where the products would stop
+    (Q = 0 makes P = 1 / (row + 1), and V = -2^-149 on the first half of the
+    keys underflows each product to -0) while V is positive further on:
+    ggml's +0 products there turn the chains, and O, into +0."""
+    import shlo_hip
+    B, H, NQ = 1, 2, NK
+    q, k, v = inputs(oracle, B, H, NQ, NK, seed=77)
+    if case == "v_inf":
+        v[0, 0, NK - 1, 7] = np.inf
+        v[0, 1, NK - 70, 40] = -np.inf
+    elif case == "v_nan":
+        v[0, 1, NK - 1, 63] = np.nan
+        v[0, 0, 100, 0] = np.nan
+    elif case == "neg_zero":
+        q[:] = 0.0
+        v[..., : NK // 2, 5] = -(2.0 ** -149)
+        v[..., NK // 2 :, 5] = 1.0
+    mask = causal(NQ, NK)
+    with np.errstate(all="ignore"):
+        want = oracle_attn(oracle, q, k, v, mask)
+    text = attn_module(B, H, NQ, NK)
+    for compile in (False, True):
+        got = run(text, [q, k, v, mask], compile=compile)
+        if not compile:
+            assert shlo_hip.last_dot_kernel() == fused_name(NK)
+        assert bits_equal(got, want, nan_ok=True), (case, compile)
+    if case == "plain":
+        assert np.isfinite(want).all()
+    elif case == "v_inf":
+        assert np.isnan(want[0, 0, : NK - 1, 7]).all() and np.isnan(want[0, 1, : NK - 70, 40]).all()
+    elif case == "v_nan":
+        assert np.isnan(want[0, 1, :, 63]).all() and np.isnan(want[0, 0, :, 0]).all()
+    else:
+        # Rows 15 .. NK/2 - 1: every chain is -0 up to key NK/2 (each product
+        # underflows), then the masked keys' +0 * 1 products make it +0;
+        # leaving those products out would give -0.
+        col = want[..., 5].view(np.uint32)
+        assert (col[:, :, 15 : NK // 2] == 0).all()
+
+
+@pytest.mark.parametrize("NK", [256, 512])
 @pytest.mark.parametrize("case", ["plain", "k_huge_masked", "k_nan_masked", "q_inf", "near_limit", "over_limit",
                                   "scale_inf", "mask_only"])
 def test_fused_attention_masked_tiles(oracle, NK, case):
