@@ -1770,40 +1770,53 @@ __device__ __forceinline__ void attn_chain_ops(const Epilogue &e, float (&v)[NV]
 // 4 (i + 16 (r / 4)) + r % 4 (i = lane % 16); an operand constant along the
 // row (s2 = 0) is one load.  Returns the 64-key slices whose P is +0 on all
 // eight rows (bit j: keys 64 j .. 64 j + 63).
+// Offset of operand value r of a lane's row (lane l: i = l % 16) in op o's
+// operand.  The element stride goes through an empty asm: left visible, the
+// compiler hoists all NV element offsets of the (rare) strided operands out
+// of the pass code and spills them.
+__device__ __forceinline__ int64_t attn_chain_off(const EpiOp &o, int64_t b, int64_t n0, int row, int r) {
+  const int li = threadIdx.x & 15;
+  int64_t s2 = o.s2;
+  asm volatile("" : "+s"(s2));
+  return b * o.s0 + (n0 + row) * o.s1 + (int64_t)(4 * (li + 16 * (r / 4)) + r % 4) * s2;
+}
+
+// The chain operands of one 16-lane row pass (see attn_chain_ops).
+template <int J>
+__device__ __forceinline__ void attn_chain_load16(const Epilogue &e1, int64_t b, int64_t n0, int row,
+                                                  float (&w)[kEpiEarly][16 * J], float (&wu)[kEpiEarly]) {
+  constexpr int NJ = 4 * J, NV = 4 * NJ;
+  const int li = threadIdx.x & 15;
+#pragma unroll
+  for (int k = 0; k < kEpiEarly; k++) {
+    if (k >= e1.n) break;
+    const EpiOp &o = e1.op[k];
+    const float *p = o.p + b * o.s0 + (n0 + row) * o.s1;
+    if (o.s2 == 0) {
+      wu[k] = *p;
+    } else if (o.s2 == 1 && ((uintptr_t)p & 15) == 0) {
+#pragma unroll
+      for (int j = 0; j < NJ; j++) {
+        const float4 f = ld4(p + 4 * (li + 16 * j));
+        w[k][4 * j] = f.x, w[k][4 * j + 1] = f.y, w[k][4 * j + 2] = f.z, w[k][4 * j + 3] = f.w;
+      }
+    } else {
+#pragma unroll
+      for (int r = 0; r < NV; r++) w[k][r] = o.p[attn_chain_off(o, b, n0, row, r)];
+    }
+  }
+}
+
+// Called before the barrier that ends phase one: the first pass's operands
+// load first, and their wait overlaps the barrier's.
 template <int J, bool UNIT>
 __device__ __forceinline__ uint32_t attn_rows16(const Epilogue &e1, float sm_sc, int64_t b, int64_t n0, float *S,
                                                 int r0) {
   constexpr int NK = 256 * J, LS = NK + 4, NJ = 4 * J, NV = 4 * NJ;
   const int lane = threadIdx.x & 63, q = lane >> 4, li = lane & 15;
-  // The element stride goes through an empty asm: left visible, the
-  // compiler hoists all NV element offsets of the (rare) strided operands out
-  // of the pass loop and spills them.
-  auto chain_off = [&](const EpiOp &o, int row, int r) {
-    int64_t s2 = o.s2;
-    asm volatile("" : "+s"(s2));
-    return b * o.s0 + (n0 + row) * o.s1 + (int64_t)(4 * (li + 16 * (r / 4)) + r % 4) * s2;
-  };
-  auto chain_load = [&](int row, float (&w)[kEpiEarly][NV], float (&wu)[kEpiEarly]) {
-#pragma unroll
-    for (int k = 0; k < kEpiEarly; k++) {
-      if (k >= e1.n) break;
-      const EpiOp &o = e1.op[k];
-      const float *p = o.p + b * o.s0 + (n0 + row) * o.s1;
-      if (o.s2 == 0) {
-        wu[k] = *p;
-      } else if (o.s2 == 1 && ((uintptr_t)p & 15) == 0) {
-#pragma unroll
-        for (int j = 0; j < NJ; j++) {
-          const float4 f = ld4(p + 4 * (li + 16 * j));
-          w[k][4 * j] = f.x, w[k][4 * j + 1] = f.y, w[k][4 * j + 2] = f.z, w[k][4 * j + 3] = f.w;
-        }
-      } else {
-#pragma unroll
-        for (int r = 0; r < NV; r++) w[k][r] = o.p[chain_off(o, row, r)];
-      }
-    }
-  };
-  float wa[kEpiEarly][NV], wb[kEpiEarly][NV], wua[kEpiEarly], wub[kEpiEarly];
+  float wa[kEpiEarly][NV], wua[kEpiEarly], wb[kEpiEarly][NV], wub[kEpiEarly];
+  attn_chain_load16<J>(e1, b, n0, r0 + q, wa, wua);
+  __syncthreads();
   auto pass = [&](int ps, const float (&w)[kEpiEarly][NV], const float (&wu)[kEpiEarly])
                   __attribute__((always_inline)) {
     const int row = r0 + 4 * ps + q;
@@ -1815,8 +1828,8 @@ __device__ __forceinline__ uint32_t attn_rows16(const Epilogue &e1, float sm_sc,
       v[4 * j] = f.x, v[4 * j + 1] = f.y, v[4 * j + 2] = f.z, v[4 * j + 3] = f.w;
     }
     attn_chain_ops(e1, v, w, wu);
-    if (ps == 0) chain_load(r0 + 4 + q, wb, wub);  // the second pass's operands load under this pass's softmax
-    epi_apply_n(e1, v, [&](const EpiOp &o, int r) { return chain_off(o, row, r); }, kEpiEarly);
+    if (ps == 0) attn_chain_load16<J>(e1, b, n0, r0 + 4 + q, wb, wub);  // loads under this pass's softmax
+    epi_apply_n(e1, v, [&](const EpiOp &o, int r) { return attn_chain_off(o, b, n0, row, r); }, kEpiEarly);
     float4 e[NJ];
 #pragma unroll
     for (int j = 0; j < NJ; j++) e[j] = make_float4(v[4 * j], v[4 * j + 1], v[4 * j + 2], v[4 * j + 3]);
@@ -1827,10 +1840,30 @@ __device__ __forceinline__ uint32_t attn_rows16(const Epilogue &e1, float sm_sc,
   };
   // Each pass has its own operand registers and both passes are inlined, so
   // the second pass's operands need no copy between the passes.
-  chain_load(r0 + q, wa, wua);
   const uint32_t z0 = pass(0, wa, wua);
   return z0 & pass(1, wb, wub);
 }
+
+// V's operands for phase three: lane l (bl = l / 16, li = l % 16) of wave w
+// takes keys 16 blk + 4 bl + g (g < 4) of value column 16 w + li, through a
+// buffer resource (one per-lane offset per g, the block in the scalar offset).
+struct AttnVLoad {
+  __amdgpu_buffer_rsrc_t r;
+  int vo[4];
+  int vstep;
+  __device__ AttnVLoad(const MfmaOperand &V, int64_t b, int wave) : r(attn_rsrc(V, b)) {
+    const int lane = threadIdx.x & 63, bl = lane >> 4, li = lane & 15;
+#pragma unroll
+    for (int g = 0; g < 4; g++) vo[g] = (int)(((int64_t)(16 * wave + li) * V.sf + (int64_t)(4 * bl + g) * V.sk) * 4);
+    vstep = (int)((int64_t)16 * V.sk * 4);  // one block of 16 keys
+  }
+  __device__ float4 operator()(int blk) const {
+    float x[4];
+#pragma unroll
+    for (int g = 0; g < 4; g++) x[g] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(r, vo[g], blk * vstep, 0));
+    return make_float4(x[0], x[1], x[2], x[3]);
+  }
+};
 
 // Phase three: O = P V in ggml order, then the chain after it, stored.  V's
 // operands load four blocks ahead of their products, in two register sets
@@ -1845,21 +1878,25 @@ __device__ __forceinline__ uint32_t attn_rows16(const Epilogue &e1, float sm_sc,
 // the wave's chains is -0 the remaining products run as well, in order.
 template <int J>
 __device__ __forceinline__ void attn_pv(const MfmaOperand &V, int64_t b, int64_t n0, int64_t NQ, int wave,
-                                        const float *S, int nzb, const Epilogue &e2, float *__restrict__ O) {
+                                        const float *S, const uint32_t *zs, uint32_t vbad, const Epilogue &e2,
+                                        float *__restrict__ O) {
   constexpr int NK = 256 * J, LS = NK + 4, NB = NK / 16;
   const int lane = threadIdx.x & 63, bl = lane >> 4, li = lane & 15;
-  const __amdgpu_buffer_rsrc_t vr = attn_rsrc(V, b);
-  int vo[4];  // the lane's byte offsets of keys 4 bl + g, column 16 wave + li
+  const AttnVLoad vl(V, b, wave);
+  auto vload = [&](int blk) { return vl(blk); };
+  // Called before the barrier that ends phase two: the first eight V blocks
+  // load first (the second four unused when the products stop at block 4).
+  float4 va[4], vb[4];
 #pragma unroll
-  for (int g = 0; g < 4; g++) vo[g] = (int)(((int64_t)(16 * wave + li) * V.sf + (int64_t)(4 * bl + g) * V.sk) * 4);
-  const int vstep = (int)((int64_t)16 * V.sk * 4);  // one block of 16 keys
-  auto vload = [&](int blk) {
-    float r[4];
+  for (int i = 0; i < 4; i++) va[i] = vload(i);
 #pragma unroll
-    for (int g = 0; g < 4; g++)
-      r[g] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(vr, vo[g], blk * vstep, 0));
-    return make_float4(r[0], r[1], r[2], r[3]);
-  };
+  for (int i = 0; i < 4; i++) vb[i] = vload(4 + i);
+  __syncthreads();
+  // Products run up to the last slice with a nonzero P on any of the 32 rows,
+  // when V is finite on the slices after it (else over all keys).
+  const uint32_t live = ~(zs[0] & zs[1] & zs[2] & zs[3]) & ((1u << (NK / 64)) - 1);
+  int nzb = live ? 4 * (32 - __builtin_clz(live)) : 4;
+  if (vbad >> (nzb / 4)) nzb = NB;
   auto pload = [&](int qt, int blk) {
     return *reinterpret_cast<const float4 *>(S + (16 * qt + li) * LS + 16 * blk + 4 * bl);
   };
@@ -1878,11 +1915,7 @@ __device__ __forceinline__ void attn_pv(const MfmaOperand &V, int64_t b, int64_t
 #pragma unroll
         for (int qt = 0; qt < 2; qt++) ps[i][qt] = pload(qt, min(blk0 + i, nzb - 1));
     };
-    float4 va[4], vb[4], pa[4][2], pb[4][2];
-#pragma unroll
-    for (int i = 0; i < 4; i++) va[i] = vload(i);
-#pragma unroll
-    for (int i = 0; i < 4; i++) vb[i] = vload(min(4 + i, nzb - 1));  // past nzb: reloads, in bounds
+    float4 pa[4][2], pb[4][2];
     pl4(pa, 0);
     pl4(pb, 4);
     pv4(va, pa, true);
@@ -1910,11 +1943,6 @@ __device__ __forceinline__ void attn_pv(const MfmaOperand &V, int64_t b, int64_t
 #pragma unroll
         for (int qt = 0; qt < 2; qt++) mfma16_block(acc[qt], pload(qt, blk0 + i), vs[i], first && i == 0);
     };
-    float4 va[4], vb[4];
-#pragma unroll
-    for (int i = 0; i < 4; i++) va[i] = vload(i);
-#pragma unroll
-    for (int i = 0; i < 4; i++) vb[i] = vload(min(4 + i, nzb - 1));  // past nzb: reloads, in bounds
     pv4(va, 0, true);
 #pragma unroll 1
     for (int b0 = 4; b0 < nzb; b0 += 8) {  // vb holds blocks b0 .. b0 + 3
@@ -1996,20 +2024,18 @@ __global__ void __launch_bounds__(256, 2) attention_k(MfmaOperand Q, MfmaOperand
   attn_qk_load(Q, Kk, b, n0, wave, st);
   const AttnSkip sk = attn_skip_plan<J>(e1, mskip, prep, b, n0, NQ, gridDim.y, wave, st);
   attn_qk<J, SKIP>(Kk, b, wave, st, S, sk);
-  __syncthreads();
+  // Global loads issued before a barrier stay in flight across it: phases
+  // two and three each start their first loads, then wait at the barrier
+  // for the other waves to finish the phase before.
   uint32_t zero = 0;  // 64-key slices whose P is +0 on this wave's rows
-  if (J <= 2)
+  if constexpr (J <= 2) {
     zero = attn_rows16<J, UNIT>(e1, sm_sc, b, n0, S, 8 * wave);
-  else
+  } else {
+    __syncthreads();
     attn_rows<J, UNIT>(e1, sm_sc, b, n0, S, 8 * wave, 8);
+  }
   if ((threadIdx.x & 63) == 0) zs[wave] = zero;
-  __syncthreads();
-  // Products run up to the last slice with a nonzero P on any of the 32 rows,
-  // when V is finite on the slices after it (else over all keys).
-  const uint32_t live = ~(zs[0] & zs[1] & zs[2] & zs[3]) & ((1u << (NK / 64)) - 1);
-  int nzb = live ? 4 * (32 - __builtin_clz(live)) : 4;
-  if (sk.vbad >> (nzb / 4)) nzb = NK / 16;
-  attn_pv<J>(V, b, n0, NQ, wave, S, nzb, e2, O);
+  attn_pv<J>(V, b, n0, NQ, wave, S, zs, sk.vbad, e2, O);
 }
 
 // ---- rows longer than 4096 columns -------------------------------------------------
