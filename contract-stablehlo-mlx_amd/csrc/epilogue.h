@@ -58,6 +58,15 @@ struct NoUnary {
   __device__ float operator()(float v) const { return v; }
 };
 
+// A chain's unary op on all NV values a lane holds.  A producer's routine
+// may overload this for its own type (found by argument-dependent lookup) to
+// share work across the values; its results must be the value-by-value ones.
+template <class Unary, int NV>
+__device__ __forceinline__ void unary_all(const Unary &un, float (&v)[NV]) {
+#pragma unroll
+  for (int r = 0; r < NV; r++) v[r] = un(v[r]);
+}
+
 // Whether an op's operand takes one value over the NV values a lane holds
 // (then one load serves them all); by default never.
 struct NeverUniform {
@@ -129,10 +138,7 @@ __device__ __forceinline__ void epi_ops_n(const Epilogue &e, float (&v)[NV], con
     if (k >= e.n) break;
     const EpiOp &o = e.op[k];
     switch (o.code) {
-      case kEpiGeluErf:
-#pragma unroll
-        for (int r = 0; r < NV; r++) v[r] = un(v[r]);
-        break;
+      case kEpiGeluErf: unary_all(un, v); break;
       case kAdd: epi_op<kAdd>(v, w[k], o.rev); break;
       case kSub: epi_op<kSub>(v, w[k], o.rev); break;
       case kMul: epi_op<kMul>(v, w[k], o.rev); break;
@@ -153,8 +159,7 @@ __device__ __forceinline__ void epi_apply_n(const Epilogue &e, float (&v)[NV], O
     if (k >= e.n) break;
     const EpiOp &o = e.op[k];
     if (o.code == kEpiGeluErf) {
-#pragma unroll
-      for (int r = 0; r < NV; r++) v[r] = un(v[r]);
+      unary_all(un, v);
       continue;
     }
     float w[NV];

@@ -72,16 +72,53 @@ __device__ __forceinline__ float gelu1(float x, const double *tab) {
   return y;
 }
 
-// Four elements at once, the same results as gelu1 element by element.
+// NV elements at once, the same results as gelu1 element by element.
 //
 // 64 |x*SQRT_2_INV| is taken as one product |x| * (64*SQRT_2_INV) (the
 // scaling is exact), clamped to 255: the same value wherever x*SQRT_2_INV is
 // a normal binary32, and where it is subnormal (|x| < 1.7e-38) erf of it is
-// below 2^-125, so 1 + ev rounds to 1 either way.  The four erf evaluations
+// below 2^-125, so 1 + ev rounds to 1 either way.  The NV erf evaluations
 // share one (rarely taken) branch into the exception table, keyed by
 // |x*SQRT_2_INV|.  NaN inputs need no select: the clamp maps them to erf = 1,
 // ev = +-1, and (0.5f*x)*(1 + ev) multiplies the quieted x, payload kept, by
 // 2 or 0, which returns it.
+template <int NV>
+__device__ __forceinline__ void gelu_erf_n(float (&x)[NV], const double *tab) {
+  uint32_t r[NV], d[NV];
+#pragma unroll
+  for (int k = 0; k < NV; k++) {
+    const float a64 = __builtin_fminf(__builtin_fabsf(x[k]) * bits_f(0x423504F3u), 255.0f);  // 64*SQRT_2_INV
+    const double R = erffk::erf_R64(a64, tab);
+    r[k] = f_bits((float)R);
+    d[k] = erffk::undecided_distance(R);
+  }
+  uint32_t dmin = d[0];
+#pragma unroll
+  for (int k = 1; k < NV; k++) dmin = dmin < d[k] ? dmin : d[k];
+  if (dmin < 0x40u) {
+#pragma unroll
+    for (int k = 0; k < NV; k++)
+      if (d[k] < 0x40u) r[k] = erffk::exception_lookup(f_bits(x[k] * bits_f(0x3F3504F3u)) & 0x7FFFFFFFu, r[k]);
+  }
+#pragma unroll
+  for (int k = 0; k < NV; k++) {
+    const float ev = bits_f(r[k] | (f_bits(x[k]) & 0x80000000u));
+    x[k] = (0.5f * x[k]) * (1.0f + ev);
+  }
+}
+
+// ggml.gelu_erf as a fused op of the dot kernels' epilogues: one output
+// through gelu1, all of a lane's outputs at once through gelu_erf_n
+// (epilogue.h's unary_all, found by argument-dependent lookup).
+struct GeluErfOp {
+  const double *tab;
+  __device__ float operator()(float x) const { return gelu1<0>(x, tab); }
+};
+template <int NV>
+__device__ __forceinline__ void unary_all(const GeluErfOp &g, float (&v)[NV]) {
+  gelu_erf_n(v, g.tab);
+}
+
 // ---- dot_general in ggml_vec_dot_f32 order --------------------------------------
 
 // The tail and the final combination shared by every dot kernel: `a` holds the
@@ -141,7 +178,7 @@ __global__ void __launch_bounds__(256) dot_ggml_simple(int64_t n_out, int64_t N,
                                                        float *__restrict__ y) {
   __shared__ double gtab[kPolyWords];  // a fused gelu_erf's table
   if (ep.gelu) load_poly(gtab);
-  auto gelu = [&](float x) { return gelu1<0>(x, gtab); };
+  const GeluErfOp gelu{gtab};
   const int64_t lk = X.sk, rk = W.sk;
   for (int64_t i = blockIdx.x * (int64_t)blockDim.x + threadIdx.x; i < n_out; i += (int64_t)gridDim.x * blockDim.x) {
     const int64_t m = i % M, t = i / M, n = t % N, b = t / N;
@@ -469,7 +506,7 @@ __device__ __forceinline__ void dot_store8(const MfmaOperand &X, const MfmaOpera
     }
   }
   if (ep.n > 0) {
-    auto gelu = [&](float x) { return gelu1<0>(x, gtab); };
+    const GeluErfOp gelu{gtab};
     if (NE > 0) epi_ops_n(ep, v, pre, gelu);
     epi_apply_n(
         ep, v, [&](const EpiOp &o, int r) { return dot_epi_off(o, b, N, M, r, row, col); }, NE, gelu,
@@ -2519,28 +2556,9 @@ __global__ void __launch_bounds__(256) silu_k(int64_t n, int64_t cols, int gpu_o
 template <int TANH>
 __device__ __forceinline__ float4 gelu4(float4 v, const double *tab) {
   if (TANH) return make_float4(gelu1<1>(v.x, tab), gelu1<1>(v.y, tab), gelu1<1>(v.z, tab), gelu1<1>(v.w, tab));
-  const float x[4] = {v.x, v.y, v.z, v.w};
-  uint32_t r[4], d[4];
-#pragma unroll
-  for (int k = 0; k < 4; k++) {
-    const float a64 = __builtin_fminf(__builtin_fabsf(x[k]) * bits_f(0x423504F3u), 255.0f);  // 64*SQRT_2_INV
-    const double R = erffk::erf_R64(a64, tab);
-    r[k] = f_bits((float)R);
-    d[k] = erffk::undecided_distance(R);
-  }
-  const uint32_t dmin = std::min(std::min(d[0], d[1]), std::min(d[2], d[3]));
-  if (dmin < 0x40u) {
-#pragma unroll
-    for (int k = 0; k < 4; k++)
-      if (d[k] < 0x40u) r[k] = erffk::exception_lookup(f_bits(x[k] * bits_f(0x3F3504F3u)) & 0x7FFFFFFFu, r[k]);
-  }
-  float y[4];
-#pragma unroll
-  for (int k = 0; k < 4; k++) {
-    const float ev = bits_f(r[k] | (f_bits(x[k]) & 0x80000000u));
-    y[k] = (0.5f * x[k]) * (1.0f + ev);
-  }
-  return make_float4(y[0], y[1], y[2], y[3]);
+  float x[4] = {v.x, v.y, v.z, v.w};
+  gelu_erf_n(x, tab);
+  return make_float4(x[0], x[1], x[2], x[3]);
 }
 
 // Block b owns the float4s [b*chunk, (b+1)*chunk) (contiguous, so each block

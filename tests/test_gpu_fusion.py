@@ -311,3 +311,55 @@ def test_planted_gelu_fault_still_differs(oracle):
     want = ch.expect(oracle, ins[0], ins[1], 0)[0]
     got = run(text, ins, faults=shlo_hip.fault_bits("gelu_tanh"))[0]
     assert not same_bits(got, want)
+
+
+def _erff_exception_keys():
+    """|x| bits of the inputs erff_cr.h decides through its exception table
+    (the rounding of its binary64 value is undecided there)."""
+    import os
+    import re
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "..", "contract-stablehlo-mlx_amd", "csrc",
+                        "erff_exceptions.h")
+    with open(path) as f:
+        return [int(k, 16) for k, _ in re.findall(r"\{0x([0-9A-F]+)u, 0x([0-9A-F]+)u\}", f.read())]
+
+
+def _gelu_inputs_on_exceptions():
+    """GELU inputs x whose erff argument RN(x * SQRT_2_INV) is an exception
+    key (both signs): the fused GELU's shared branch into the table."""
+    c = np.array([0x3F3504F3], np.uint32).view(F32)[0]
+    out = []
+    for k in _erff_exception_keys():
+        a = np.array([k], np.uint32).view(F32)[0]
+        x0 = F32(np.float64(a) / np.float64(c))
+        cand = [x0]
+        for _ in range(3):
+            cand += [np.nextafter(cand[-1], F32(np.inf)), np.nextafter(cand[0], F32(0))]
+        for x in cand:
+            if F32(x * c) == a:
+                out += [x, -x]
+                break
+    return np.array(out, F32)
+
+
+@pytest.mark.parametrize("N,K,M", [(256, 512, 192), (130, 1024, 70), (33, 33, 9)])
+def test_gelu_on_exception_inputs_and_nan_payloads(oracle, N, K, M):
+    """[x 0, + operand, gelu_erf]: the GELU's input is the operand exactly, so
+    every value below reaches it: inputs whose erff takes the exception table,
+    NaN payloads (quiet and signalling, both signs), +-inf, +-0, subnormals and
+    values past erf's clamp.  The four-wave and eight-wave direct kernels
+    evaluate a lane's eight GELUs together (one branch into the table, NaN
+    through the clamp); the one-thread-per-output kernel one at a time."""
+    exc = _gelu_inputs_on_exceptions()
+    assert len(exc) >= 100, len(exc)
+    special = np.array([0x7FC00000, 0xFFC00001, 0x7F800001, 0xFF812345, 0x7FFFFFFF, 0x7F800000, 0xFF800000,
+                        0x00000000, 0x80000000, 0x00000001, 0x807FFFFF, 0x00400000, 0x7F7FFFFF, 0xC0A00000,
+                        0x40800000, 0x3F800000], np.uint32).view(F32)
+    res = normal(oracle, 63, (N, M), 2.0)
+    flat = res.reshape(-1)
+    vals = np.concatenate([exc, special])
+    rng = np.random.default_rng(7)
+    pos = rng.permutation(flat.size)[:min(flat.size, 3 * vals.size)]
+    flat[pos] = np.resize(vals, pos.size)
+    ops = [("multiply", scalar(0.0), ("bcast", ()), False), ("add", res, None, False), ("gelu", None, None, False)]
+    check(oracle, Chain((), N, K, M, ops))
