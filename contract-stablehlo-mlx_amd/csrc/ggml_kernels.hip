@@ -2046,11 +2046,16 @@ __global__ void __launch_bounds__(256, 2) attention_k(MfmaOperand Q, MfmaOperand
     // A heavy block's waves wait on their own dependences as much as they
     // issue, and a light block fills those gaps, where two light blocks
     // together would leave the CU mostly idle.  Consecutive ranks walk the
-    // batches.
+    // batches.  The lightest ranks go in reverse order within each aligned
+    // run of 8 ids, which keeps every id's rank congruent to the id mod 8
+    // (C is a multiple of 8; so is nb whenever the batch count is): XCD x,
+    // which takes the ids = x mod 8, then computes only batches = x mod 8
+    // (for a batch count that is a multiple of 8), and their K and V stay in
+    // its L2.  Every mapping here is a bijection on the grid.
     const uint32_t lin = blockIdx.x + gridDim.x * blockIdx.y;
     const uint32_t nb = gridDim.x * gridDim.y, C = 256;
     uint32_t h = lin;
-    if (nb >= 2 * C) h = lin < C ? lin : lin < 2 * C ? nb - 1 - (lin - C) : lin - C;
+    if (nb >= 2 * C) h = lin < C ? lin : lin < 2 * C ? nb - 1 - ((lin - C) ^ 7u) : lin - C;
     ty = h % gridDim.y;
     tx = gridDim.x - 1 - h / gridDim.y;
   } else if (gridDim.y > 1) {

@@ -753,7 +753,7 @@ struct Lowerer {
       if (p < 0) continue;
       const Op &pv = b.ops[p];
       if (pv.name != "stablehlo.dot_general" || !fusable_producer(pv) || pv.operands[0] != sm.results[0] ||
-          pv.operands[1] == sm.results[0] || fu->skip[p] && fu->chain[p].empty())
+          pv.operands[1] == sm.results[0] || (fu->skip[p] && fu->chain[p].empty()))
         continue;
       AttnGroup g{(int)i, s, p, ch1, fu->chain[p]};
       const int last = g.ch2.empty() ? p : g.ch2.back();
