@@ -523,3 +523,35 @@ def test_fused_attention_masked_tiles(oracle, NK, case):
         assert np.isfinite(want).all()
     if case in ("k_nan_masked", "q_inf", "over_limit", "scale_inf"):
         assert np.isnan(want).any()
+
+
+@pytest.mark.parametrize("case", ["plain", "v_inf"])
+def test_fused_attention_unaligned_v(oracle, case):
+    """V as a view whose rows are not 16-byte aligned (columns 1 .. 64 of a
+    65-wide argument, read in place): attn_prep_k's finiteness check and P V's
+    buffer loads at odd offsets.  With an infinite value among the masked keys
+    P V must not leave those products out."""
+    import shlo_hip
+    B, H, NQ, NK = 2, 2, 256, 256
+    q, k, v = inputs(oracle, B, H, NQ, NK, seed=79)
+    if case == "v_inf":
+        v[1, 0, NK - 3, 17] = np.inf
+    wide = np.concatenate([np.full((B, H, NK, 1), F32(5.0)), v], axis=3)
+    text = attn_module(B, H, NQ, NK)
+    vw = t((B, H, NK, 65))
+    text = text.replace(f"%v: {t((B, H, NK, 64))}", f"%vw: {vw}", 1)
+    text = text.replace(
+        "    %0 = ",
+        f'    %v = "stablehlo.slice"(%vw) {{start_indices = array<i64: 0, 0, 0, 1>, limit_indices = '
+        f"array<i64: {B}, {H}, {NK}, 65>, strides = array<i64: 1, 1, 1, 1>}} : ({vw}) -> {t((B, H, NK, 64))}\n"
+        "    %0 = ", 1)
+    mask = causal(NQ, NK)
+    with np.errstate(all="ignore"):
+        want = oracle_attn(oracle, q, k, v, mask)
+    for compile in (False, True):
+        got = run(text, [q, k, wide, mask], compile=compile)
+        if not compile:
+            assert shlo_hip.last_dot_kernel() == fused_name(NK)
+        assert bits_equal(got, want, nan_ok=True), (case, compile)
+    if case == "v_inf":
+        assert np.isnan(want[1, 0, : NK - 3, 17]).all()
