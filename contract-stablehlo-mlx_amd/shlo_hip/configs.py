@@ -45,6 +45,16 @@ def unary_module(target, attrs, dims):
 SOFTMAX_SCALE1 = "scale = 0x3F800000 : f32"
 
 
+def unary_many_module(target, attrs, dims, n):
+    """n independent applications of one ggml.* custom call, argument i to
+    result i (a cold stream: each launch reads its own input)."""
+    ty = t(dims)
+    args = ", ".join(f"%a{i}: {ty}" for i in range(n))
+    body = "".join(custom_call(f"%{i}", f"%a{i}", target, attrs, ty) for i in range(n))
+    rets, tys = ", ".join(f"%{i}" for i in range(n)), ", ".join(ty for _ in range(n))
+    return f"module {{\n  func.func public @main({args}) -> ({tys}) {{\n{body}    func.return {rets} : {tys}\n  }}\n}}\n"
+
+
 def hot_path_module(rows=4096, cols=1024, n_gelu=64 << 20):
     """ggml.soft_max over [rows, cols] and ggml.gelu_erf
     over n_gelu elements, one module (one graph)."""
