@@ -50,10 +50,12 @@ constexpr uint32_t kClampBits = 0x407F0000u;
 
 // R ~ erf(a64 / 64) in binary64 for a64 in [0, 255] (a quiet NaN is clamped
 // there by the callers' v_min_f32 / fminf, which return the number),
-// branch-free: i = floor(a64), u = a64 - i, R = a64 * (Q_i(u) / 64) with row i
-// of `tab` holding Q_i / 64.  u is exact (the fraction of a binary64 copy of a
-// binary32).
-__host__ __device__ inline double erf_R64(float a64, const double *tab) {
+// branch-free: i = floor(a64), u = a64 - i, R = a64 * (Q_i(u) / 64) with
+// row(i) pointing at Q_i / 64's six coefficients (tab + 6 i for a whole
+// table; a caller may hold the table in pieces).  u is exact (the fraction of
+// a binary64 copy of a binary32).
+template <class Row>
+__host__ __device__ inline double erf_R64_at(float a64, Row row) {
   const double ad = (double)a64;
 #if defined(__HIP_DEVICE_COMPILE__)
   const double u = __builtin_amdgcn_fract(ad);  // ad - floor(ad), exact for ad >= 0
@@ -61,7 +63,7 @@ __host__ __device__ inline double erf_R64(float a64, const double *tab) {
   const double u = ad - __builtin_floor(ad);
 #endif
   const unsigned i = (unsigned)(int)a64 & (unsigned)(kTab - 1);
-  const double *p = tab + 6 * i;
+  const double *p = row(i);
   double q = p[5];
   q = __builtin_fma(q, u, p[4]);
   q = __builtin_fma(q, u, p[3]);
@@ -69,6 +71,10 @@ __host__ __device__ inline double erf_R64(float a64, const double *tab) {
   q = __builtin_fma(q, u, p[1]);
   q = __builtin_fma(q, u, p[0]);
   return ad * q;
+}
+
+__host__ __device__ inline double erf_R64(float a64, const double *tab) {
+  return erf_R64_at(a64, [tab](unsigned i) { return tab + 6 * i; });
 }
 
 // R ~ erf(min(a, kClampA)) for a = |x| >= 0 or a quiet NaN.

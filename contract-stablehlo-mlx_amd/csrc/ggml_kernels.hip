@@ -82,13 +82,14 @@ __device__ __forceinline__ float gelu1(float x, const double *tab) {
 // |x*SQRT_2_INV|.  NaN inputs need no select: the clamp maps them to erf = 1,
 // ev = +-1, and (0.5f*x)*(1 + ev) multiplies the quieted x, payload kept, by
 // 2 or 0, which returns it.
-template <int NV>
-__device__ __forceinline__ void gelu_erf_n(float (&x)[NV], const double *tab) {
+// row(i): the erff table's row i (erffk::erf_R64_at).
+template <int NV, class Row>
+__device__ __forceinline__ void gelu_erf_n_at(float (&x)[NV], Row row) {
   uint32_t r[NV], d[NV];
 #pragma unroll
   for (int k = 0; k < NV; k++) {
     const float a64 = __builtin_fminf(__builtin_fabsf(x[k]) * bits_f(0x423504F3u), 255.0f);  // 64*SQRT_2_INV
-    const double R = erffk::erf_R64(a64, tab);
+    const double R = erffk::erf_R64_at(a64, row);
     r[k] = f_bits((float)R);
     d[k] = erffk::undecided_distance(R);
   }
@@ -106,6 +107,10 @@ __device__ __forceinline__ void gelu_erf_n(float (&x)[NV], const double *tab) {
     x[k] = (0.5f * x[k]) * (1.0f + ev);
   }
 }
+template <int NV>
+__device__ __forceinline__ void gelu_erf_n(float (&x)[NV], const double *tab) {
+  gelu_erf_n_at(x, [tab](unsigned i) { return tab + 6 * i; });
+}
 
 // ggml.gelu_erf as a fused op of the dot kernels' epilogues: one output
 // through gelu1, all of a lane's outputs at once through gelu_erf_n
@@ -117,6 +122,26 @@ struct GeluErfOp {
 template <int NV>
 __device__ __forceinline__ void unary_all(const GeluErfOp &g, float (&v)[NV]) {
   gelu_erf_n(v, g.tab);
+}
+
+// The same with the table held in two pieces of LDS: rows 0 .. 127 at lo,
+// 128 .. 255 at hi (the four-wave matrix kernel stages it in its two free
+// lhs stage buffers for the epilogue).
+constexpr int kPolyHalfRows = erffk::kTab / 2;
+struct GeluErfSplitOp {
+  const double *lo, *hi;
+  __device__ const double *row(unsigned i) const {
+    return i < (unsigned)kPolyHalfRows ? lo + 6 * i : hi + 6 * (i - kPolyHalfRows);
+  }
+  __device__ float operator()(float x) const {
+    float v[1] = {x};
+    gelu_erf_n_at(v, [this](unsigned i) { return row(i); });
+    return v[0];
+  }
+};
+template <int NV>
+__device__ __forceinline__ void unary_all(const GeluErfSplitOp &g, float (&v)[NV]) {
+  gelu_erf_n_at(v, [&g](unsigned i) { return g.row(i); });
 }
 
 // ---- dot_general in ggml_vec_dot_f32 order --------------------------------------
@@ -471,12 +496,13 @@ __device__ __forceinline__ void dot_epi_early(const Epilogue &ep, int64_t b, int
 // col(r), after the serial tail of dot_finish when K % 16 != 0 and the fused
 // element-wise ops (the first kEpiEarly with operands `pre` loaded by
 // dot_epi_early).  `whole` (wave-uniform) says every output is in range and
-// there is no tail.
-template <bool COLCONST, int NE = kEpiEarly, class RowF, class ColF>
+// there is no tail.  `gelu` is a fused ggml.gelu_erf's routine (GeluErfOp or
+// GeluErfSplitOp, by where the kernel holds the erff table).
+template <bool COLCONST, int NE = kEpiEarly, class Gelu, class RowF, class ColF>
 __device__ __forceinline__ void dot_store8(const MfmaOperand &X, const MfmaOperand &W, int64_t b, int64_t N,
                                            int64_t M, int64_t K, int64_t np, int tail, bool whole,
                                            const float (&out)[8], const Epilogue &ep, const float (&pre)[kEpiEarly][8],
-                                           const double *gtab, float *__restrict__ Y, RowF row, ColF col) {
+                                           const Gelu &gelu, float *__restrict__ Y, RowF row, ColF col) {
   float v[8];
 #pragma unroll
   for (int r = 0; r < 8; r++) v[r] = out[r];
@@ -506,7 +532,6 @@ __device__ __forceinline__ void dot_store8(const MfmaOperand &X, const MfmaOpera
     }
   }
   if (ep.n > 0) {
-    const GeluErfOp gelu{gtab};
     if (NE > 0) epi_ops_n(ep, v, pre, gelu);
     epi_apply_n(
         ep, v, [&](const EpiOp &o, int r) { return dot_epi_off(o, b, N, M, r, row, col); }, NE, gelu,
@@ -640,8 +665,8 @@ __global__ void __launch_bounds__(512) dot_mfma8_k(MfmaOperand X, MfmaOperand W,
     }
     out[r] = (w[0] + w[1]) + (w[2] + w[3]);  // vaddvq_f32
   }
-  dot_store8<true>(X, W, b, N, M, K, np, tail, np == K && n0 + kMT <= N && m0 + kMT <= M, out, ep, pre, gtab, Y, orow,
-             ocol);
+  dot_store8<true>(X, W, b, N, M, K, np, tail, np == K && n0 + kMT <= N && m0 + kMT <= M, out, ep, pre,
+                   GeluErfOp{gtab}, Y, orow, ocol);
 }
 
 
@@ -742,8 +767,12 @@ __global__ void __launch_bounds__(WAVES * 64, 2) dot_mfma8d_k(MfmaOperand X, Mfm
   auto ocol = [&](int) { return ml; };
   float pre[kEpiEarly][8];
   if (NE > 0) dot_epi_early<true>(ep, b, N, M, pre, orow, ocol);
-  // The four-wave form reads a fused GELU's table from global memory (cached),
-  // keeping its LDS at 48 KB so that three workgroups share a CU.
+  // A fused GELU's erff table: the eight-wave form stages it in dynamic LDS
+  // at the start.  The four-wave form keeps its LDS at 48 KB, so that three
+  // workgroups share a CU: with edge tiles it reads the table from global
+  // memory (cached); without, it stages the table after the products in its
+  // lhs stage buffers (LDS_TAB below).
+  constexpr bool LDS_TAB = WAVES == 4 && !EDGE;
   const double *gt = WAVES == 4 ? &erffk::kPoly[0][0] : gtab;
   if (WAVES == 8 && ep.gelu) load_poly(gtab);
 
@@ -835,6 +864,22 @@ __global__ void __launch_bounds__(WAVES * 64, 2) dot_mfma8d_k(MfmaOperand X, Mfm
     if (s + 1 < nst) stage(dx1, dw1, dx0, dw0, s + 1);
   }
 
+  // LDS_TAB with a fused GELU: after the last stage's barrier no wave reads
+  // the lhs stage buffers and no load into them is outstanding, so the erff
+  // table (768 float4s, three per thread) goes there: rows 0 .. 127 to dx0,
+  // 128 .. 255 to dx1 (6 KB each).  Loaded now, stored with the exchange,
+  // before its barrier.
+  static_assert(!LDS_TAB || (WAVES * 64 == 256 && kPolyWords / 2 == 3 * 256 &&
+                             kPolyHalfRows * 6 / 2 == 384 && 384 <= XCH),
+                "the erff table's halves fit the lhs stage buffers, three float4s per thread");
+  const bool stage_tab = LDS_TAB && ep.gelu;
+  float4 tq[3];
+  if (stage_tab) {
+    const float4 *src = reinterpret_cast<const float4 *>(&erffk::kPoly[0][0]);
+#pragma unroll
+    for (int j = 0; j < 3; j++) tq[j] = src[threadIdx.x + 256 * j];
+  }
+
   // Epilogue: dot_mfma8_k's, the exchange in the lhs buffers (waves 0..3 in
   // dx0, 4..7 in dx1; four waves: the rhs buffers; no load is outstanding
   // after the last stage).
@@ -851,6 +896,13 @@ __global__ void __launch_bounds__(WAVES * 64, 2) dot_mfma8d_k(MfmaOperand X, Mfm
   for (int r = 0; r < 8; r++)
 #pragma unroll
     for (int q = 0; q < 4; q++) give[(r * 4 + q) * 64 + lane] = rh ? t4[r][q] : t4[8 + r][q];
+  if (stage_tab) {
+#pragma unroll
+    for (int j = 0; j < 3; j++) {
+      const int q = threadIdx.x + 256 * j;
+      *(q < 384 ? dx0 + q : dx1 + (q - 384)) = tq[j];
+    }
+  }
   __syncthreads();
   // EDGE with a tail: the tile's tail operands (lhs rows n0.., rhs rows m0..,
   // k in [np, K)) go to LDS once, in the buffers the exchange leaves free
@@ -906,7 +958,12 @@ __global__ void __launch_bounds__(WAVES * 64, 2) dot_mfma8d_k(MfmaOperand X, Mfm
     }
   }
   const bool whole = !EDGE || (n0 + TN <= N && m0 + kMT <= M);
-  dot_store8<true, NE>(X, W, b, N, M, K, K, tail, whole, out, ep, pre, gt, Y, orow, ocol);
+  if constexpr (LDS_TAB) {
+    const GeluErfSplitOp gelu{reinterpret_cast<const double *>(dx0), reinterpret_cast<const double *>(dx1)};
+    dot_store8<true, NE>(X, W, b, N, M, K, K, tail, whole, out, ep, pre, gelu, Y, orow, ocol);
+  } else {
+    dot_store8<true, NE>(X, W, b, N, M, K, K, tail, whole, out, ep, pre, GeluErfOp{gt}, Y, orow, ocol);
+  }
 }
 
 
