@@ -2083,9 +2083,11 @@ __device__ __forceinline__ void attn_pv(const MfmaOperand &V, int64_t b, int64_t
 
 // One workgroup of four waves per block, the phases in turn.  Consecutive
 // query blocks of one batch share K and V: each XCD takes a contiguous run of
-// workgroups (whole batches), whose K and V stay in its L2.
+// workgroups (whole batches), whose K and V stay in its L2.  Scores of 256 or
+// 512 keys (33 or 66 KB of LDS) let two or more workgroups share a CU; 768 or
+// 1024 keys (99 or 132 KB) leave room for one, and the register budget says so.
 template <int J, bool UNIT, bool SKIP>
-__global__ void __launch_bounds__(256, 2) attention_k(MfmaOperand Q, MfmaOperand Kk, MfmaOperand V, int64_t NQ,
+__global__ void __launch_bounds__(256, J <= 2 ? 2 : 1) attention_k(MfmaOperand Q, MfmaOperand Kk, MfmaOperand V, int64_t NQ,
                                                       Epilogue e1, int mskip, const int *__restrict__ prep,
                                                       float sm_sc, Epilogue e2, float *__restrict__ O) {
   constexpr int NK = 256 * J, LS = NK + 4;
