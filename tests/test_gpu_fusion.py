@@ -342,14 +342,22 @@ def _gelu_inputs_on_exceptions():
     return np.array(out, F32)
 
 
-@pytest.mark.parametrize("N,K,M", [(256, 512, 192), (130, 1024, 70), (33, 33, 9)])
-def test_gelu_on_exception_inputs_and_nan_payloads(oracle, N, K, M):
+@pytest.mark.parametrize("N,K,M,kernel", [(256, 512, 192, "dot_mfma8d_k<RowVecB,ColQuadB,64,4>"),
+                                          (128, 132, 128, "dot_mfma8d_k<RowVecB,ColQuadB,64,4>"),
+                                          (128, 1024, 192, "dot_mfma8d_k<RowVecB,ColQuadB,128,8>"),
+                                          (130, 1024, 70, "dot_mfma8_k<"),
+                                          (33, 33, 9, None)])
+def test_gelu_on_exception_inputs_and_nan_payloads(oracle, N, K, M, kernel):
     """[x 0, + operand, gelu_erf]: the GELU's input is the operand exactly, so
     every value below reaches it: inputs whose erff takes the exception table,
     NaN payloads (quiet and signalling, both signs), +-inf, +-0, subnormals and
-    values past erf's clamp.  The four-wave and eight-wave direct kernels
-    evaluate a lane's eight GELUs together (one branch into the table, NaN
-    through the clamp); the one-thread-per-output kernel one at a time."""
+    values past erf's clamp.  The matrix kernels evaluate a lane's eight
+    GELUs together (one branch into the table, NaN through the clamp), with
+    the erff table staged in LDS after the products (the four-wave direct
+    kernel, whole tiles), read from global memory (the same with a tail),
+    or staged in LDS from the start (the eight-wave direct kernel, the
+    register-staged kernel); the kernel of the last shape evaluates them one
+    at a time."""
     exc = _gelu_inputs_on_exceptions()
     assert len(exc) >= 100, len(exc)
     special = np.array([0x7FC00000, 0xFFC00001, 0x7F800001, 0xFF812345, 0x7FFFFFFF, 0x7F800000, 0xFF800000,
@@ -362,4 +370,8 @@ def test_gelu_on_exception_inputs_and_nan_payloads(oracle, N, K, M):
     pos = rng.permutation(flat.size)[:min(flat.size, 3 * vals.size)]
     flat[pos] = np.resize(vals, pos.size)
     ops = [("multiply", scalar(0.0), ("bcast", ()), False), ("add", res, None, False), ("gelu", None, None, False)]
-    check(oracle, Chain((), N, K, M, ops))
+    text, ins = check(oracle, Chain((), N, K, M, ops))
+    if kernel is not None:
+        import shlo_hip
+        run(text, ins, compile=False)
+        assert shlo_hip.last_dot_kernel().startswith(kernel), shlo_hip.last_dot_kernel()
