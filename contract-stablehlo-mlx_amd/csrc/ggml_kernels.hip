@@ -866,18 +866,23 @@ __global__ void __launch_bounds__(WAVES * 64, 2) dot_mfma8d_k(MfmaOperand X, Mfm
 
   // LDS_TAB with a fused GELU: after the last stage's barrier no wave reads
   // the lhs stage buffers and no load into them is outstanding, so the erff
-  // table (768 float4s, three per thread) goes there: rows 0 .. 127 to dx0,
-  // 128 .. 255 to dx1 (6 KB each).  Loaded now, stored with the exchange,
-  // before its barrier.
-  static_assert(!LDS_TAB || (WAVES * 64 == 256 && kPolyWords / 2 == 3 * 256 &&
-                             kPolyHalfRows * 6 / 2 == 384 && 384 <= XCH),
-                "the erff table's halves fit the lhs stage buffers, three float4s per thread");
+  // table goes there, straight from memory (buffer_load_dwordx4 lds, no
+  // registers): twelve 1 KB chunks, three per wave, chunks 0 .. 5 (rows
+  // 0 .. 127) to dx0 and 6 .. 11 (rows 128 .. 255) to dx1.  The wave waits for
+  // its chunks before the exchange's barrier.
+  static_assert(!LDS_TAB || (WAVES == 4 && kPolyWords * 8 == 12 * 1024 && kPolyHalfRows * 6 * 8 == 6 * 1024 &&
+                             6 * 64 <= XCH),
+                "the erff table is twelve 1 KB chunks, six per lhs stage buffer, three per wave");
   const bool stage_tab = LDS_TAB && ep.gelu;
-  float4 tq[3];
   if (stage_tab) {
-    const float4 *src = reinterpret_cast<const float4 *>(&erffk::kPoly[0][0]);
+    const __amdgpu_buffer_rsrc_t tr = __builtin_amdgcn_make_buffer_rsrc(
+        (void *)&erffk::kPoly[0][0], (short)0, kPolyWords * (int)sizeof(double), 0x00020000);
 #pragma unroll
-    for (int j = 0; j < 3; j++) tq[j] = src[threadIdx.x + 256 * j];
+    for (int j = 0; j < 3; j++) {
+      const int c = 4 * j + wv;  // wave-uniform
+      float4 *dst = c < 6 ? dx0 + 64 * c : dx1 + 64 * (c - 6);
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(tr, (lds_void *)dst, 16, 16 * lane, 1024 * c, 0, 0);
+    }
   }
 
   // Epilogue: dot_mfma8_k's, the exchange in the lhs buffers (waves 0..3 in
@@ -896,13 +901,7 @@ __global__ void __launch_bounds__(WAVES * 64, 2) dot_mfma8d_k(MfmaOperand X, Mfm
   for (int r = 0; r < 8; r++)
 #pragma unroll
     for (int q = 0; q < 4; q++) give[(r * 4 + q) * 64 + lane] = rh ? t4[r][q] : t4[8 + r][q];
-  if (stage_tab) {
-#pragma unroll
-    for (int j = 0; j < 3; j++) {
-      const int q = threadIdx.x + 256 * j;
-      *(q < 384 ? dx0 + q : dx1 + (q - 384)) = tq[j];
-    }
-  }
+  if (stage_tab) __builtin_amdgcn_s_waitcnt(0);  // this wave's table chunks have landed in LDS
   __syncthreads();
   // EDGE with a tail: the tile's tail operands (lhs rows n0.., rhs rows m0..,
   // k in [np, K)) go to LDS once, in the buffers the exchange leaves free
