@@ -1977,13 +1977,16 @@ __device__ __forceinline__ void attn_pv(const MfmaOperand &V, int64_t b, int64_t
   const int lane = threadIdx.x & 63, bl = lane >> 4, li = lane & 15;
   const AttnVLoad vl(V, b, wave);
   auto vload = [&](int blk) { return vl(blk); };
-  // Called before the barrier that ends phase two: the first eight V blocks
-  // load first (the second four unused when the products stop at block 4).
-  float4 va[4], vb[4];
+  // Called before the barrier that ends phase two: the first V blocks load
+  // first (eight in two sets of four; for 256 keys four in two sets of two,
+  // which keeps the kernel within three workgroups' registers per CU).  A
+  // second set goes unused when the products stop after the first.
+  constexpr int VS = J >= 2 ? 4 : 2;  // V blocks per register set
+  float4 va[VS], vb[VS];
 #pragma unroll
-  for (int i = 0; i < 4; i++) va[i] = vload(i);
+  for (int i = 0; i < VS; i++) va[i] = vload(i);
 #pragma unroll
-  for (int i = 0; i < 4; i++) vb[i] = vload(4 + i);
+  for (int i = 0; i < VS; i++) vb[i] = vload(VS + i);
   __syncthreads();
   // Products run up to the last slice with a nonzero P on any of the 32 rows,
   // when V is finite on the slices after it (else over all keys).
@@ -2029,23 +2032,25 @@ __device__ __forceinline__ void attn_pv(const MfmaOperand &V, int64_t b, int64_t
       __builtin_amdgcn_sched_barrier(0);
     }
   } else {
-    // Block 0 starts the accumulators from the inline +0 (first).
-    auto pv4 = [&](const float4 (&vs)[4], int blk0, bool first) {
+    // Sets of VS = 2 blocks, in block order; block 0 starts the accumulators
+    // from the inline +0 (first).  nzb is a multiple of 4, so the sets end on
+    // it; loads past it reload block nzb - 1 (in range, unused).
+    auto pvs = [&](const float4 (&vs)[VS], int blk0, bool first) {
 #pragma unroll
-      for (int i = 0; i < 4; i++)
+      for (int i = 0; i < VS; i++)
 #pragma unroll
         for (int qt = 0; qt < 2; qt++) mfma16_block(acc[qt], pload(qt, blk0 + i), vs[i], first && i == 0);
     };
-    pv4(va, 0, true);
+    pvs(va, 0, true);
 #pragma unroll 1
-    for (int b0 = 4; b0 < nzb; b0 += 8) {  // vb holds blocks b0 .. b0 + 3
+    for (int b0 = VS; b0 < nzb; b0 += 2 * VS) {  // vb holds blocks b0 .. b0 + VS - 1
 #pragma unroll
-      for (int i = 0; i < 4; i++) va[i] = vload(min(b0 + 4 + i, nzb - 1));
-      pv4(vb, b0, false);
-      if (b0 + 4 >= nzb) break;
+      for (int i = 0; i < VS; i++) va[i] = vload(min(b0 + VS + i, nzb - 1));
+      pvs(vb, b0, false);
+      if (b0 + VS >= nzb) break;
 #pragma unroll
-      for (int i = 0; i < 4; i++) vb[i] = vload(min(b0 + 8 + i, nzb - 1));
-      pv4(va, b0 + 4, false);
+      for (int i = 0; i < VS; i++) vb[i] = vload(min(b0 + 2 * VS + i, nzb - 1));
+      pvs(va, b0 + VS, false);
     }
   }
   if (nzb < NB) {
@@ -2082,11 +2087,12 @@ __device__ __forceinline__ void attn_pv(const MfmaOperand &V, int64_t b, int64_t
 
 // One workgroup of four waves per block, the phases in turn.  Consecutive
 // query blocks of one batch share K and V: each XCD takes a contiguous run of
-// workgroups (whole batches), whose K and V stay in its L2.  Scores of 256 or
-// 512 keys (33 or 66 KB of LDS) let two or more workgroups share a CU; 768 or
-// 1024 keys (99 or 132 KB) leave room for one, and the register budget says so.
+// workgroups (whole batches), whose K and V stay in its L2.  The register
+// budget follows the workgroups per CU that the scores' LDS allows, up to
+// three: 256 keys (33 KB) three, 512 keys (66 KB) two, 768 or 1024 keys (99
+// or 132 KB) one.
 template <int J, bool UNIT, bool SKIP>
-__global__ void __launch_bounds__(256, J <= 2 ? 2 : 1) attention_k(MfmaOperand Q, MfmaOperand Kk, MfmaOperand V, int64_t NQ,
+__global__ void __launch_bounds__(256, J == 1 ? 3 : J == 2 ? 2 : 1) attention_k(MfmaOperand Q, MfmaOperand Kk, MfmaOperand V, int64_t NQ,
                                                       Epilogue e1, int mskip, const int *__restrict__ prep,
                                                       float sm_sc, Epilogue e2, float *__restrict__ O) {
   constexpr int NK = 256 * J, LS = NK + 4;
