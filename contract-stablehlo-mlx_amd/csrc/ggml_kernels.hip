@@ -2453,9 +2453,15 @@ __global__ void __launch_bounds__(256) norm_rows_k(int64_t rows, int cols, float
                            : make_float4(0.0f, 0.0f, 0.0f, 0.0f);
   }
   const float et = lane < T ? x[4 * G + lane] : 0.0f;
-  // The fused ops' operands do not depend on the row's sums: their loads go
-  // out now and land under the reductions.
+  // The fused ops' operands do not depend on the row's sums.  For rows of
+  // more than 512 columns their loads go out now and land under the
+  // reductions; for 512 and fewer they go out after the sums (LATE): held
+  // through the reductions, their registers would keep the kernel above 64,
+  // the budget at which all eight waves per SIMD of a [8192, 512] row set
+  // are resident at once.
+  constexpr bool LATE = J <= 2;
   float w[kEpiEarly][4 * J], wt[kEpiEarly][1];  // the first kEpiEarly ops' operands; later ops load at the end
+  auto load_ops = [&]() {
   if (EPI) {
     // An operand along columns with unit stride from a 16-byte aligned start
     // (LayerNorm's gain and bias) loads float4 groups, as the row does;
@@ -2484,6 +2490,8 @@ __global__ void __launch_bounds__(256) norm_rows_k(int64_t rows, int cols, float
     }
     if (T > 0) epi_load_n(ep, wt, [&](const EpiOp &o, int) { return row * o.s1 + (lane < T ? 4 * G + lane : 0) * o.s2; });
   }
+  };
+  if (!LATE) load_ops();
   double ls = 0.0, la = 0.0;
   int le = 255;
   auto take = [&](float v) {
@@ -2559,6 +2567,7 @@ __global__ void __launch_bounds__(256) norm_rows_k(int64_t rows, int cols, float
   const float dt = et - mean, qt = dt * dt;
   const double dc = (double)cols;
   const float var = ordered_sum_apply<J, FULL>(part, G, qt, T, [dc](double v) { return (float)(v / dc); });
+  if (LATE) load_ops();
   const float scl = 1.0f / sqrtf(var + eps);
   float v[4 * J];
 #pragma unroll
