@@ -2092,9 +2092,9 @@ __device__ __forceinline__ void attn_pv(const MfmaOperand &V, int64_t b, int64_t
 // three: 256 keys (33 KB) three, 512 keys (66 KB) two, 768 or 1024 keys (99
 // or 132 KB) one.
 template <int J, bool UNIT, bool SKIP>
-__global__ void __launch_bounds__(256, J == 1 ? 3 : J == 2 ? 2 : 1) attention_k(MfmaOperand Q, MfmaOperand Kk, MfmaOperand V, int64_t NQ,
-                                                      Epilogue e1, int mskip, const int *__restrict__ prep,
-                                                      float sm_sc, Epilogue e2, float *__restrict__ O) {
+__global__ void __launch_bounds__(256, J == 1 ? 3 : J == 2 ? 2 : 1)
+    attention_k(MfmaOperand Q, MfmaOperand Kk, MfmaOperand V, int64_t NQ, Epilogue e1, int mskip,
+                const int *__restrict__ prep, float sm_sc, Epilogue e2, float *__restrict__ O) {
   constexpr int NK = 256 * J, LS = NK + 4;
   __shared__ __attribute__((aligned(16))) float S[kAttnRows * LS];
   __shared__ uint32_t zs[4];
@@ -2462,34 +2462,35 @@ __global__ void __launch_bounds__(256) norm_rows_k(int64_t rows, int cols, float
   constexpr bool LATE = J <= 2;
   float w[kEpiEarly][4 * J], wt[kEpiEarly][1];  // the first kEpiEarly ops' operands; later ops load at the end
   auto load_ops = [&]() {
-  if (EPI) {
-    // An operand along columns with unit stride from a 16-byte aligned start
-    // (LayerNorm's gain and bias) loads float4 groups, as the row does;
-    // any other, one element at a time.
+    if (EPI) {
+      // An operand along columns with unit stride from a 16-byte aligned start
+      // (LayerNorm's gain and bias) loads float4 groups, as the row does;
+      // any other, one element at a time.
 #pragma unroll
-    for (int k = 0; k < kEpiEarly; k++) {
-      if (k >= ep.n) break;
-      const EpiOp &o = ep.op[k];
-      if (o.code == kEpiGeluErf) continue;
-      const float *base = o.p + row * o.s1;
-      if (o.s2 == 1 && T == 0 && ((uintptr_t)base & 15) == 0) {
+      for (int k = 0; k < kEpiEarly; k++) {
+        if (k >= ep.n) break;
+        const EpiOp &o = ep.op[k];
+        if (o.code == kEpiGeluErf) continue;
+        const float *base = o.p + row * o.s1;
+        if (o.s2 == 1 && T == 0 && ((uintptr_t)base & 15) == 0) {
 #pragma unroll
-        for (int j = 0; j < J; j++) {
-          const int g = lane + kWave * j;
-          const float4 q = ld4(base + 4 * ((FULL || g < G) ? g : 0));  // a discarded group reads group 0
-          w[k][4 * j] = q.x, w[k][4 * j + 1] = q.y, w[k][4 * j + 2] = q.z, w[k][4 * j + 3] = q.w;
-        }
-      } else {
+          for (int j = 0; j < J; j++) {
+            const int g = lane + kWave * j;
+            const float4 q = ld4(base + 4 * ((FULL || g < G) ? g : 0));  // a discarded group reads group 0
+            w[k][4 * j] = q.x, w[k][4 * j + 1] = q.y, w[k][4 * j + 2] = q.z, w[k][4 * j + 3] = q.w;
+          }
+        } else {
 #pragma unroll
-        for (int r = 0; r < 4 * J; r++) {
-          const int g = lane + kWave * (r / 4);
-          const int c = (FULL || g < G) ? 4 * g + r % 4 : 0;  // a discarded group reads column 0
-          w[k][r] = o.p[row * o.s1 + c * o.s2];
+          for (int r = 0; r < 4 * J; r++) {
+            const int g = lane + kWave * (r / 4);
+            const int c = (FULL || g < G) ? 4 * g + r % 4 : 0;  // a discarded group reads column 0
+            w[k][r] = o.p[row * o.s1 + c * o.s2];
+          }
         }
       }
+      if (T > 0)
+        epi_load_n(ep, wt, [&](const EpiOp &o, int) { return row * o.s1 + (lane < T ? 4 * G + lane : 0) * o.s2; });
     }
-    if (T > 0) epi_load_n(ep, wt, [&](const EpiOp &o, int) { return row * o.s1 + (lane < T ? 4 * G + lane : 0) * o.s2; });
-  }
   };
   if (!LATE) load_ops();
   double ls = 0.0, la = 0.0;
